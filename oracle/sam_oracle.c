@@ -1,0 +1,376 @@
+/*
+ * CPU oracle: plain-C restatement of the reference CPU path for the fused-attention hot path.
+ * Test infrastructure only (checker and CPU baseline); the product never links it.
+ *
+ * Compiled with -ffp-contract=off so that `x*scale + rh + rw` rounds after every operation, as the
+ * reference's Rust does (Rust never contracts to FMA). The tile GEMMs live in oracle_gemm.c.
+ */
+#include "sam_oracle.h"
+
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* oracle_gemm.c */
+void oracle_gemm_rows(const float* a, const float* b, float* c, int rows, int k, int n);
+
+static int threads_or_all(int nthreads) {
+#ifdef _OPENMP
+  return nthreads > 0 ? nthreads : omp_get_max_threads();
+#else
+  (void)nthreads;
+  return 1;
+#endif
+}
+
+/* Sequential f32 dot product, in the order `tab.iter().zip(q).map(|(a, b)| a * b).sum()` uses
+ * (kernels.rs:77, 190). */
+static float dot_seq(const float* a, const float* b, int n) {
+  float acc = 0.0f;
+  for (int c = 0; c < n; ++c) acc += a[c] * b[c];
+  return acc;
+}
+
+/* kernels.rs:75-83 / 187-196: rh[kh] = q . th[i + h-1 - kh], rw[kw] = q . tw[j + w-1 - kw]. */
+static void rel_bias_row(const float* qr, const float* th, const float* tw, int h, int w, int hd, int i, int j,
+                         float* rh, float* rw) {
+  for (int kh = 0; kh < h; ++kh) rh[kh] = dot_seq(th + (long)(i + h - 1 - kh) * hd, qr, hd);
+  for (int kw = 0; kw < w; ++kw) rw[kw] = dot_seq(tw + (long)(j + w - 1 - kw) * hd, qr, hd);
+}
+
+/* kernels.rs:84-101 / 197-214: x = s*scale + rh[kh] + rw[kw]; max; exp(x - max); sum; x *= 1/sum. */
+static void softmax_relpos_row(const float* s, float* o, const float* rh, const float* rw, int h, int w,
+                               float scale) {
+  const int n = h * w;
+  float mx = -INFINITY;
+  for (int kh = 0; kh < h; ++kh) {
+    for (int kw = 0; kw < w; ++kw) {
+      float v = s[kh * w + kw] * scale;
+      v = v + rh[kh];
+      v = v + rw[kw];
+      o[kh * w + kw] = v;
+      mx = fmaxf(mx, v);
+    }
+  }
+  float sum = 0.0f;
+  for (int k = 0; k < n; ++k) {
+    o[k] = expf(o[k] - mx);
+    sum += o[k];
+  }
+  const float inv = 1.0f / sum;
+  for (int k = 0; k < n; ++k) o[k] *= inv;
+}
+
+void oracle_relpos_softmax(const float* s, const float* q, const float* table, float* out, long bh, int h, int w,
+                           int hd, float scale, int nthreads) {
+  const int n = h * w;
+  const float* th = table;
+  const float* tw = table + (long)(2 * h - 1) * hd;
+  const long rows = bh * n;
+#pragma omp parallel num_threads(threads_or_all(nthreads))
+  {
+    float* rh = (float*)malloc(sizeof(float) * (size_t)h);
+    float* rw = (float*)malloc(sizeof(float) * (size_t)w);
+#pragma omp for schedule(static)
+    for (long row = 0; row < rows; ++row) {
+      const int rem = (int)(row % n), i = rem / w, j = rem % w;
+      rel_bias_row(q + row * hd, th, tw, h, w, hd, i, j, rh, rw);
+      softmax_relpos_row(s + row * n, out + row * n, rh, rw, h, w, scale);
+    }
+    free(rh);
+    free(rw);
+  }
+}
+
+/* kernels.rs:116 (TILE) and 157-221: one task per (head, 32-row query tile). */
+#define ORACLE_TILE 32
+
+void oracle_attention_relpos(const float* q, const float* kt, const float* v, const float* table, float* out, long bh,
+                             int h, int w, int hd, float scale, int nthreads) {
+  const int n = h * w;
+  const float* th = table;
+  const float* tw = table + (long)(2 * h - 1) * hd;
+  const long tiles = (n + ORACLE_TILE - 1) / ORACLE_TILE;
+  const long tasks = bh * tiles;
+#pragma omp parallel num_threads(threads_or_all(nthreads))
+  {
+    float* sc = (float*)malloc(sizeof(float) * (size_t)ORACLE_TILE * n);
+    float* rh = (float*)malloc(sizeof(float) * (size_t)h);
+    float* rw = (float*)malloc(sizeof(float) * (size_t)w);
+#pragma omp for schedule(dynamic, 1)
+    for (long task = 0; task < tasks; ++task) {
+      const long b = task / tiles, t = task % tiles;
+      const int r0 = (int)(t * ORACLE_TILE);
+      const int rows = n - r0 < ORACLE_TILE ? n - r0 : ORACLE_TILE;
+      const float* qb = q + (b * n + r0) * (long)hd;
+      const float* ktb = kt + b * (long)hd * n;
+      const float* vb = v + b * (long)n * hd;
+      float* o = out + (b * n + r0) * (long)hd;
+      /* scores[rows, n] = q_tile[rows, hd] @ kt[hd, n]   (kernels.rs:181-185) */
+      oracle_gemm_rows(qb, ktb, sc, rows, hd, n);
+      for (int r = 0; r < rows; ++r) {
+        const int row = r0 + r, i = row / w, j = row % w;
+        rel_bias_row(qb + (long)r * hd, th, tw, h, w, hd, i, j, rh, rw);
+        softmax_relpos_row(sc + (long)r * n, sc + (long)r * n, rh, rw, h, w, scale);
+      }
+      /* out_tile[rows, hd] = probs[rows, n] @ v[n, hd]   (kernels.rs:216-220) */
+      oracle_gemm_rows(sc, vb, o, rows, n, hd);
+    }
+    free(sc);
+    free(rh);
+    free(rw);
+  }
+}
+
+void oracle_qkv_split(const float* y, const float* bias, float* out, long tokens, int n, int nh, int hd, int nthreads) {
+  const long c = (long)nh * hd;
+  const long plane = tokens * c;
+#pragma omp parallel for schedule(static) num_threads(threads_or_all(nthreads))
+  for (long t = 0; t < tokens; ++t) {
+    const long win = t / n, tok = t % n;
+    for (int which = 0; which < 3; ++which) {
+      for (int head = 0; head < nh; ++head) {
+        const long bhi = win * nh + head;
+        for (int d = 0; d < hd; ++d) {
+          const long col = which * c + (long)head * hd + d;
+          const long dst = which == 1 ? (bhi * hd + d) * n + tok : (bhi * n + tok) * hd + d;
+          out[which * plane + dst] = y[t * 3 * c + col] + bias[col];
+        }
+      }
+    }
+  }
+}
+
+void oracle_deform_attn(const float* value, const float* loc, const float* attn, float* out, int b, int s, int q, int h,
+                        int d, int l, int p, const int* shapes, int nthreads) {
+  long starts[64];
+  long acc = 0;
+  for (int li = 0; li < l; ++li) {
+    starts[li] = acc;
+    acc += (long)shapes[2 * li] * shapes[2 * li + 1];
+  }
+  const long bq_total = (long)b * q;
+#pragma omp parallel for schedule(static) num_threads(threads_or_all(nthreads))
+  for (long bq = 0; bq < bq_total; ++bq) {
+    const long bi = bq / q;
+    float* o = out + bq * (long)h * d;
+    memset(o, 0, sizeof(float) * (size_t)h * d);
+    for (int hi = 0; hi < h; ++hi) {
+      float* a = o + (long)hi * d;
+      for (int li = 0; li < l; ++li) {
+        const int hl = shapes[2 * li], wl = shapes[2 * li + 1];
+        for (int pi = 0; pi < p; ++pi) {
+          const long base = ((bq * h + hi) * l + li) * p + pi;
+          const float wgt = attn[base];
+          const float x = loc[base * 2] * (float)wl - 0.5f;
+          const float y = loc[base * 2 + 1] * (float)hl - 0.5f;
+          const float xf = floorf(x), yf = floorf(y);
+          const long x0 = (long)xf, y0 = (long)yf;
+          const float fx = x - xf, fy = y - yf;
+          for (int c = 0; c < 4; ++c) {
+            const long xx = x0 + (c & 1), yy = y0 + (c >> 1);
+            if (xx < 0 || xx >= wl || yy < 0 || yy >= hl) continue;
+            /* kernels.rs:805: w * wx * wy, left to right */
+            float wt = wgt * ((c & 1) ? fx : 1.0f - fx);
+            wt = wt * ((c >> 1) ? fy : 1.0f - fy);
+            const float* src = value + ((bi * s + starts[li] + yy * wl + xx) * h + hi) * (long)d;
+            for (int e = 0; e < d; ++e) a[e] += wt * src[e];
+          }
+        }
+      }
+    }
+  }
+}
+
+/* candle's softmax_last_dim on CPU: max, exp(x - max), sum, x / sum. */
+static void softmax_div(float* x, int n) {
+  float mx = -INFINITY;
+  for (int k = 0; k < n; ++k) mx = fmaxf(mx, x[k]);
+  float sum = 0.0f;
+  for (int k = 0; k < n; ++k) {
+    x[k] = expf(x[k] - mx);
+    sum += x[k];
+  }
+  for (int k = 0; k < n; ++k) x[k] = x[k] / sum;
+}
+
+void oracle_sdpa(const float* q, const float* k, const float* v, float* out, int b, int h, int lq, int lk, int d,
+                 int nthreads) {
+  const float scale = powf((float)d, -0.5f);
+  const long heads = (long)b * h;
+  const long tiles = (lq + ORACLE_TILE - 1) / ORACLE_TILE;
+#pragma omp parallel num_threads(threads_or_all(nthreads))
+  {
+    float* kt = (float*)malloc(sizeof(float) * (size_t)d * lk);
+    float* sc = (float*)malloc(sizeof(float) * (size_t)ORACLE_TILE * lk);
+    long cur = -1;
+#pragma omp for schedule(static)
+    for (long task = 0; task < heads * tiles; ++task) {
+      const long bh = task / tiles, t = task % tiles;
+      const float* kb = k + bh * (long)lk * d;
+      if (bh != cur) { /* k.transpose(2, 3).contiguous() (nn.rs:28) */
+        for (int j = 0; j < lk; ++j)
+          for (int c = 0; c < d; ++c) kt[(long)c * lk + j] = kb[(long)j * d + c];
+        cur = bh;
+      }
+      const int r0 = (int)(t * ORACLE_TILE);
+      const int rows = lq - r0 < ORACLE_TILE ? lq - r0 : ORACLE_TILE;
+      oracle_gemm_rows(q + (bh * lq + r0) * (long)d, kt, sc, rows, d, lk);
+      for (int r = 0; r < rows; ++r) {
+        float* row = sc + (long)r * lk;
+        for (int j = 0; j < lk; ++j) row[j] = row[j] * scale; /* (q k^T) * scale (nn.rs:28) */
+        softmax_div(row, lk);
+      }
+      oracle_gemm_rows(sc, v + bh * (long)lk * d, out + (bh * lq + r0) * (long)d, rows, lk, d);
+    }
+    free(kt);
+    free(sc);
+  }
+}
+
+void oracle_mha_blhd(const float* q, const float* k, const float* v, float* out, int b, int lq, int lk, int h, int d,
+                     float scale, int nthreads) {
+  const long e = (long)h * d;
+  const long tasks = (long)b * lq * h;
+#pragma omp parallel num_threads(threads_or_all(nthreads))
+  {
+    float* sc = (float*)malloc(sizeof(float) * (size_t)lk);
+#pragma omp for schedule(static)
+    for (long task = 0; task < tasks; ++task) {
+      const long bi = task / ((long)lq * h);
+      const long qi = (task / h) % lq, head = task % h;
+      const float* qv = q + (bi * lq + qi) * e + head * d;
+      float* o = out + (bi * lq + qi) * e + head * d;
+      float mx = -INFINITY;
+      for (int j = 0; j < lk; ++j) {
+        const float* kv = k + (bi * lk + j) * e + head * d;
+        const float s = dot_seq(qv, kv, d) * scale;
+        sc[j] = s;
+        mx = fmaxf(mx, s);
+      }
+      float sum = 0.0f;
+      for (int j = 0; j < lk; ++j) {
+        sc[j] = expf(sc[j] - mx);
+        sum += sc[j];
+      }
+      const float inv = 1.0f / sum;
+      for (int c = 0; c < d; ++c) o[c] = 0.0f;
+      for (int j = 0; j < lk; ++j) {
+        const float pj = sc[j] * inv;
+        const float* vv = v + (bi * lk + j) * e + head * d;
+        for (int c = 0; c < d; ++c) o[c] += pj * vv[c];
+      }
+    }
+    free(sc);
+  }
+}
+
+void oracle_rope_tables(int side, float scale, int hd, float theta, float* cos_out, float* sin_out) {
+  const int sp = hd / 2;
+  float inv[1024];
+  for (int i = 0; i < sp / 2; ++i) inv[i] = 1.0f / powf(theta, 2.0f * (float)i / (float)sp);
+  for (int r = 0; r < side; ++r) {
+    for (int c = 0; c < side; ++c) {
+      const long t = (long)r * side + c;
+      for (int j = 0; j < sp; ++j) {
+        const float pos = j < sp / 2 ? (float)c * scale : (float)r * scale;
+        const float f = j < sp / 2 ? inv[j] : inv[j - sp / 2];
+        const float a = pos * f;
+        for (int kk = 0; kk < 2; ++kk) { /* repeat_interleave(2) */
+          cos_out[t * hd + 2 * j + kk] = cosf(a);
+          sin_out[t * hd + 2 * j + kk] = sinf(a);
+        }
+      }
+    }
+  }
+}
+
+void oracle_rope(const float* x, const float* cos_t, const float* sin_t, float* out, long l, int d) {
+  for (long t = 0; t < l; ++t) {
+    const float* xr = x + t * d;
+    for (int c = 0; c < d; c += 2) {
+      const float x0 = xr[c], x1 = xr[c + 1];
+      /* x*cos + rot*sin with rot = [-x1, x0] (video.rs:110-112) */
+      float a = x0 * cos_t[t * d + c];
+      float b = -x1 * sin_t[t * d + c];
+      out[t * d + c] = a + b;
+      a = x1 * cos_t[t * d + c + 1];
+      b = x0 * sin_t[t * d + c + 1];
+      out[t * d + c + 1] = a + b;
+    }
+  }
+}
+
+void oracle_rope_attention(const float* q, const float* k, const float* v, const float* cos_t, const float* sin_t,
+                           int trows, float* out, int lq, int mk, int d, int n_exclude, int nthreads) {
+  float* qr = (float*)malloc(sizeof(float) * (size_t)lq * d);
+  float* kr = (float*)malloc(sizeof(float) * (size_t)mk * d);
+  oracle_rope(q, cos_t, sin_t, qr, lq, d);
+  const int rot = mk - n_exclude;
+  for (int r0 = 0; r0 < rot; r0 += trows) { /* tables tiled `rot / trows` times (video.rs:137-139) */
+    const int len = rot - r0 < trows ? rot - r0 : trows;
+    oracle_rope(k + (long)r0 * d, cos_t, sin_t, kr + (long)r0 * d, len, d);
+  }
+  memcpy(kr + (long)rot * d, k + (long)rot * d, sizeof(float) * (size_t)n_exclude * d);
+  oracle_sdpa(qr, kr, v, out, 1, 1, lq, mk, d, nthreads);
+  free(qr);
+  free(kr);
+}
+
+/* IEEE binary16 round-to-nearest-even, returned as f32 (gcc has no _Float16 on x86 here). */
+static float round_to_f16(float x) {
+  if (isnan(x)) return x;
+  const float ax = fabsf(x);
+  if (ax >= 65520.0f) return copysignf(INFINITY, x); /* halfway between 65504 and 2^16 rounds up */
+  float quantum;
+  if (ax < 6.103515625e-05f) {
+    quantum = 5.9604644775390625e-08f; /* subnormal spacing 2^-24 */
+  } else {
+    int e;
+    frexpf(ax, &e); /* ax in [2^(e-1), 2^e): 11 significant bits -> spacing 2^(e-11) */
+    quantum = ldexpf(1.0f, e - 11);
+  }
+  return copysignf(nearbyintf(ax / quantum) * quantum, x);
+}
+
+void oracle_round_f16(float* x, long n) {
+  for (long i = 0; i < n; ++i) x[i] = round_to_f16(x[i]);
+}
+
+void oracle_round_bf16(float* x, long n) {
+  for (long i = 0; i < n; ++i) {
+    uint32_t b;
+    memcpy(&b, &x[i], 4);
+    if (isnan(x[i])) {
+      b = (b | 0x00400000u) & 0xffff0000u;
+    } else {
+      b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
+    }
+    memcpy(&x[i], &b, 4);
+  }
+}
+
+static uint64_t splitmix64(uint64_t* st) {
+  uint64_t z = (*st += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+void oracle_randn(unsigned long long seed, float* out, long n, float mean, float std) {
+  uint64_t st = seed;
+  for (long i = 0; i < n; i += 2) {
+    /* two uniforms in (0, 1]: 53-bit mantissas */
+    const double u1 = ((double)(splitmix64(&st) >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+    const double u2 = (double)(splitmix64(&st) >> 11) * (1.0 / 9007199254740992.0);
+    const double r = sqrt(-2.0 * log(u1));
+    const double a = 6.283185307179586 * u2;
+    out[i] = (float)(mean + std * r * cos(a));
+    if (i + 1 < n) out[i + 1] = (float)(mean + std * r * sin(a));
+  }
+}

@@ -1,0 +1,183 @@
+"""ctypes front end of the CPU oracle (liboracle.so).
+
+Test infrastructure only: the test suite, the smoke check and the CPU-baseline leg of the benchmark
+use it as the checker. The product (libsam_hip.so and sam_hip.py) never imports it.
+
+Every function takes and returns contiguous float32 numpy arrays and cites the reference lines its C
+implementation restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_F = ctypes.POINTER(ctypes.c_float)
+_I = ctypes.POINTER(ctypes.c_int)
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the Makefile beside this file."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-B" if force else "all"], cwd=_HERE, check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle library not built: {_LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(_LIB_PATH)
+        L.oracle_relpos_softmax.argtypes = [_F, _F, _F, _F, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_float, ctypes.c_int]
+        L.oracle_attention_relpos.argtypes = [_F, _F, _F, _F, _F, ctypes.c_long, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_float, ctypes.c_int]
+        L.oracle_qkv_split.argtypes = [_F, _F, _F, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int]
+        L.oracle_deform_attn.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 7 + [_I, ctypes.c_int]
+        L.oracle_sdpa.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 6
+        L.oracle_mha_blhd.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int]
+        L.oracle_rope_tables.argtypes = [ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_float, _F, _F]
+        L.oracle_rope.argtypes = [_F, _F, _F, _F, ctypes.c_long, ctypes.c_int]
+        L.oracle_rope_attention.argtypes = [_F, _F, _F, _F, _F, ctypes.c_int, _F] + [ctypes.c_int] * 5
+        L.oracle_round_f16.argtypes = [_F, ctypes.c_long]
+        L.oracle_round_bf16.argtypes = [_F, ctypes.c_long]
+        L.oracle_randn.argtypes = [ctypes.c_ulonglong, _F, ctypes.c_long, ctypes.c_float, ctypes.c_float]
+        _lib = L
+    return _lib
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(_F)
+
+
+def relpos_softmax(s, q, table, h: int, w: int, scale: float, nthreads: int = 0) -> np.ndarray:
+    """kernels.rs:62-105. s [BH, N, N], q [BH, N, hd], table [(2h-1)+(2w-1), hd] -> [BH, N, N]."""
+    s, q, table = _f32(s), _f32(q), _f32(table)
+    bh, n, hd = q.shape
+    assert n == h * w and s.shape == (bh, n, n) and table.shape == (2 * h - 1 + 2 * w - 1, hd)
+    out = np.empty_like(s)
+    lib().oracle_relpos_softmax(_p(s), _p(q), _p(table), _p(out), bh, h, w, hd, scale, nthreads)
+    return out
+
+
+def attention_relpos(q, kt, v, table, h: int, w: int, scale: float, nthreads: int = 0) -> np.ndarray:
+    """kernels.rs:181-220 (exact f32 TiledAttention). q [BH,N,hd], kt [BH,hd,N], v [BH,N,hd] -> [BH,N,hd]."""
+    q, kt, v, table = _f32(q), _f32(kt), _f32(v), _f32(table)
+    bh, n, hd = q.shape
+    assert n == h * w and kt.shape == (bh, hd, n) and v.shape == (bh, n, hd)
+    assert table.shape == (2 * h - 1 + 2 * w - 1, hd)
+    out = np.empty_like(q)
+    lib().oracle_attention_relpos(_p(q), _p(kt), _p(v), _p(table), _p(out), bh, h, w, hd, scale, nthreads)
+    return out
+
+
+def qkv_split(y, bias, n: int, nh: int, hd: int, nthreads: int = 0):
+    """kernels.rs:239-263. y [T, 3*nh*hd], bias [3*nh*hd] -> (q [BH,n,hd], kT [BH,hd,n], v [BH,n,hd])."""
+    y, bias = _f32(y), _f32(bias)
+    t = y.shape[0]
+    assert y.shape == (t, 3 * nh * hd) and bias.shape == (3 * nh * hd,) and t % n == 0
+    out = np.empty((3, t * nh * hd), np.float32)
+    lib().oracle_qkv_split(_p(y), _p(bias), _p(out), t, n, nh, hd, nthreads)
+    bh = t // n * nh
+    return out[0].reshape(bh, n, hd), out[1].reshape(bh, hd, n), out[2].reshape(bh, n, hd)
+
+
+def deform_attn(value, loc, attn, shapes, nthreads: int = 0) -> np.ndarray:
+    """kernels.rs:776-818. value [B,S,H,D], loc [B,Q,H,L,P,2], attn [B,Q,H,L,P] -> [B,Q,H*D]."""
+    value, loc, attn = _f32(value), _f32(loc), _f32(attn)
+    b, s, h, d = value.shape
+    q, l, p = loc.shape[1], loc.shape[3], loc.shape[4]
+    assert loc.shape == (b, q, h, l, p, 2) and attn.shape == (b, q, h, l, p) and len(shapes) == l
+    assert sum(hh * ww for hh, ww in shapes) == s
+    sh = np.ascontiguousarray(np.array(shapes, np.int32).reshape(-1))
+    out = np.empty((b, q, h * d), np.float32)
+    lib().oracle_deform_attn(_p(value), _p(loc), _p(attn), _p(out), b, s, q, h, d, l, p, sh.ctypes.data_as(_I),
+                             nthreads)
+    return out
+
+
+def sdpa(q, k, v, nthreads: int = 0) -> np.ndarray:
+    """sam3/nn.rs:26-34 with mask None. q [B,H,Lq,D], k/v [B,H,Lk,D] -> [B,H,Lq,D]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    b, h, lq, d = q.shape
+    lk = k.shape[2]
+    assert k.shape == (b, h, lk, d) and v.shape == k.shape
+    out = np.empty_like(q)
+    lib().oracle_sdpa(_p(q), _p(k), _p(v), _p(out), b, h, lq, lk, d, nthreads)
+    return out
+
+
+def mha_blhd(q, k, v, scale: float | None = None, nthreads: int = 0) -> np.ndarray:
+    """kernels.rs:416-434 / 502-548 semantics on [B, L, H, D] (the flash-attention layout)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    b, lq, h, d = q.shape
+    lk = k.shape[1]
+    assert k.shape == (b, lk, h, d) and v.shape == k.shape
+    if scale is None:
+        scale = float(d) ** -0.5
+    out = np.empty_like(q)
+    lib().oracle_mha_blhd(_p(q), _p(k), _p(v), _p(out), b, lq, lk, h, d, scale, nthreads)
+    return out
+
+
+def rope_tables(side: int, scale: float, hd: int, theta: float):
+    """sam3/vision.rs:26-46 -> (cos, sin), each [side*side, hd]."""
+    cos = np.empty((side * side, hd), np.float32)
+    sin = np.empty((side * side, hd), np.float32)
+    lib().oracle_rope_tables(side, scale, hd, theta, _p(cos), _p(sin))
+    return cos, sin
+
+
+def rope(x, cos, sin) -> np.ndarray:
+    """sam3/video.rs:106-113 on x [L, D] with cos/sin [L, D]."""
+    x, cos, sin = _f32(x), _f32(cos), _f32(sin)
+    l, d = x.shape
+    assert cos.shape == (l, d) and sin.shape == (l, d)
+    out = np.empty_like(x)
+    lib().oracle_rope(_p(x), _p(cos), _p(sin), _p(out), l, d)
+    return out
+
+
+def rope_attention(q, k, v, cos, sin, n_exclude: int, nthreads: int = 0) -> np.ndarray:
+    """sam3/video.rs:129-145 after the projections: q [Lq, D], k/v [M, D]; one head."""
+    q, k, v, cos, sin = _f32(q), _f32(k), _f32(v), _f32(cos), _f32(sin)
+    lq, d = q.shape
+    mk = k.shape[0]
+    trows = cos.shape[0]
+    assert lq == trows and (mk - n_exclude) % trows == 0
+    out = np.empty_like(q)
+    lib().oracle_rope_attention(_p(q), _p(k), _p(v), _p(cos), _p(sin), trows, _p(out), lq, mk, d, n_exclude,
+                                nthreads)
+    return out
+
+
+def round_to(x, dtype: str) -> np.ndarray:
+    """Round f32 values to f16 or bf16 (round-to-nearest-even) and return them as f32."""
+    x = np.array(x, dtype=np.float32, copy=True, order="C")
+    if dtype == "f16":
+        lib().oracle_round_f16(_p(x), x.size)
+    elif dtype == "bf16":
+        lib().oracle_round_bf16(_p(x), x.size)
+    elif dtype != "f32":
+        raise ValueError(dtype)
+    return x
+
+
+def randn(seed: int, shape, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    """SplitMix64 + Box-Muller normals: the seeded synthetic-input generator."""
+    n = int(np.prod(shape))
+    out = np.empty(n, np.float32)
+    lib().oracle_randn(seed, _p(out), n, mean, std)
+    return out.reshape(shape)

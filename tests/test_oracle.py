@@ -1,0 +1,337 @@
+"""Pins the CPU oracle before anything is checked against it (CPU only).
+
+Each oracle function is compared with an independent float64 formulation (tests/refimpl.py), with
+closed forms and special cases, and with brute force on tiny inputs. The `*_mutants_are_caught` tests
+plant plausible mistakes (a flipped index sign, swapped tables, a dropped bias term, a transposed
+operand, ...) in a copy of the formula, on the CPU, and check that the comparison used here would
+reject each of them.
+"""
+import numpy as np
+import pytest
+
+import refimpl
+
+RELPOS_GEOMS = [(2, 3, 1, 8), (7, 11, 2, 80), (14, 14, 2, 64), (1, 5, 2, 16), (64, 64, 1, 80)]
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _relpos_inputs(h, w, bh, hd, seed, table_std=0.5):
+    r = _rng(seed)
+    n = h * w
+    q = r.standard_normal((bh, n, hd)).astype(np.float32)
+    kt = r.standard_normal((bh, hd, n)).astype(np.float32)
+    v = r.standard_normal((bh, n, hd)).astype(np.float32)
+    table = (table_std * r.standard_normal((2 * h - 1 + 2 * w - 1, hd))).astype(np.float32)
+    return q, kt, v, table
+
+
+@pytest.mark.parametrize("h,w,bh,hd", RELPOS_GEOMS)
+def test_textbook_and_fallback_index_forms_agree(h, w, bh, hd):
+    q, kt, _, table = _relpos_inputs(h, w, bh, hd, 1)
+    s = q.astype(np.float64) @ kt
+    a = refimpl.relpos_logits64(s, q, table, h, w, 0.3)
+    b = refimpl.relpos_logits_fallback_index64(s, q, table, h, w, 0.3)
+    np.testing.assert_allclose(a, b, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("h,w,bh,hd", RELPOS_GEOMS[:4])
+def test_relpos_softmax_matches_textbook(oracle_lib, h, w, bh, hd):
+    q, kt, _, table = _relpos_inputs(h, w, bh, hd, 2)
+    s = (q @ kt).astype(np.float32)
+    scale = hd ** -0.5
+    got = oracle_lib.relpos_softmax(s, q, table, h, w, scale)
+    want = refimpl.relpos_softmax64(s, q, table, h, w, scale)
+    assert np.abs(got - want).max() < 2e-6
+    np.testing.assert_allclose(got.sum(-1), 1.0, atol=1e-5)
+
+
+@pytest.mark.parametrize("h,w,bh,hd", RELPOS_GEOMS)
+def test_attention_relpos_matches_textbook(oracle_lib, h, w, bh, hd):
+    q, kt, v, table = _relpos_inputs(h, w, bh, hd, 3)
+    scale = hd ** -0.5
+    got = oracle_lib.attention_relpos(q, kt, v, table, h, w, scale)
+    want = refimpl.attention_relpos64(q, kt, v, table, h, w, scale)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    # f32 rounding of the 4096-key logits and sums alone is ~6e-6 of max|out| at 64x64
+    assert err < (2e-6 if h * w <= 256 else 1e-5), err
+
+
+def test_attention_relpos_zero_table_is_plain_attention(oracle_lib):
+    q, kt, v, table = _relpos_inputs(7, 11, 2, 80, 4)
+    table[:] = 0
+    scale = 0.125
+    got = oracle_lib.attention_relpos(q, kt, v, table, 7, 11, scale)
+    want = refimpl.sdpa64(q, np.swapaxes(kt, 1, 2), v, scale=scale)
+    assert np.abs(got - want).max() < 2e-6
+
+
+def test_attention_relpos_uniform_when_scale_and_table_are_zero(oracle_lib):
+    q, kt, v, table = _relpos_inputs(14, 14, 2, 64, 5)
+    table[:] = 0
+    got = oracle_lib.attention_relpos(q, kt, v, table, 14, 14, 0.0)
+    want = np.broadcast_to(v.astype(np.float64).mean(axis=1, keepdims=True), v.shape)
+    assert np.abs(got - want).max() < 1e-6
+
+
+def test_attention_relpos_one_hot_values_recover_probabilities(oracle_lib):
+    h, w = 2, 3
+    n = h * w
+    q, kt, _, table = _relpos_inputs(h, w, 2, n, 6)
+    v = np.broadcast_to(np.eye(n, dtype=np.float32), (2, n, n)).copy()
+    got = oracle_lib.attention_relpos(q, kt, v, table, h, w, 0.4)
+    probs = oracle_lib.relpos_softmax((q @ kt).astype(np.float32), q, table, h, w, 0.4)
+    assert np.abs(got - probs).max() < 1e-6
+
+
+def test_attention_relpos_bias_depends_only_on_offsets():
+    """A table whose rows are one-hot in a channel that q selects gives bias = table value at the
+    relative offset: check one hand-computed logit of the textbook form."""
+    h, w, hd = 3, 4, 2
+    table = np.zeros((2 * h - 1 + 2 * w - 1, hd))
+    table[: 2 * h - 1, 0] = np.arange(2 * h - 1) * 10.0  # rel_pos_h values 0, 10, ..., in channel 0
+    table[2 * h - 1:, 1] = np.arange(2 * w - 1) * 1.0  # rel_pos_w values 0, 1, ..., in channel 1
+    q = np.ones((1, h * w, hd))
+    s = np.zeros((1, h * w, h * w))
+    logits = refimpl.relpos_logits64(s, q, table, h, w, 1.0)
+    # query (i=2, j=1) vs key (kh=0, kw=3): rel_pos_h[i-kh+h-1] = rel_pos_h[4] = 40, rel_pos_w[j-kw+w-1] = [1] = 1
+    assert logits[0, 2 * w + 1, 0 * w + 3] == 41.0
+
+
+def _mutants():
+    def flip_sign(s, q, table, h, w, scale):  # kh - i instead of i - kh
+        t = table.copy()
+        t[: 2 * h - 1] = t[: 2 * h - 1][::-1]
+        t[2 * h - 1:] = t[2 * h - 1:][::-1]
+        return refimpl.relpos_logits64(s, q, t, h, w, scale)
+
+    def swap_tables(s, q, table, h, w, scale):  # table split in the wrong order (rel_pos_w rows first)
+        t = np.concatenate([table[2 * h - 1:], table[: 2 * h - 1]])
+        return refimpl.relpos_logits64(s, q, t, h, w, scale)
+
+    def drop_rw(s, q, table, h, w, scale):
+        t = table.copy()
+        t[2 * h - 1:] = 0
+        return refimpl.relpos_logits64(s, q, t, h, w, scale)
+
+    def drop_rh(s, q, table, h, w, scale):
+        t = table.copy()
+        t[: 2 * h - 1] = 0
+        return refimpl.relpos_logits64(s, q, t, h, w, scale)
+
+    def scale_bias_too(s, q, table, h, w, scale):  # scale applied to the bias as well
+        return refimpl.relpos_logits64(s, q, table * scale, h, w, scale)
+
+    def transposed_keys(s, q, table, h, w, scale):
+        return refimpl.relpos_logits64(np.swapaxes(s, 1, 2), q, table, h, w, scale)
+
+    return [flip_sign, swap_tables, drop_rw, drop_rh, scale_bias_too, transposed_keys]
+
+
+@pytest.mark.parametrize("mutant", _mutants(), ids=lambda f: f.__name__)
+def test_relpos_mutants_are_caught(oracle_lib, mutant):
+    h, w, bh, hd = 7, 11, 1, 80
+    q, kt, _, table = _relpos_inputs(h, w, bh, hd, 7)
+    s = (q @ kt).astype(np.float32)
+    got = oracle_lib.relpos_softmax(s, q, table, h, w, 0.125)
+    bad = refimpl.softmax64(mutant(s.astype(np.float64), q, table, h, w, 0.125))
+    assert np.abs(got - bad).max() > 1e-3  # far above the 2e-6 the real comparison allows
+
+
+# ----------------------------------------------------------------------------------------- qkv split
+
+def test_qkv_split_is_the_reference_permutation(oracle_lib):
+    n, nh, hd, win = 196, 3, 16, 2
+    r = _rng(8)
+    y = r.standard_normal((win * n, 3 * nh * hd)).astype(np.float32)
+    b = r.standard_normal(3 * nh * hd).astype(np.float32)
+    q, kt, v = oracle_lib.qkv_split(y, b, n, nh, hd)
+    qkv = (y + b).reshape(win, n, 3, nh, hd).transpose(2, 0, 3, 1, 4).reshape(3, win * nh, n, hd)
+    assert np.array_equal(q, qkv[0])
+    assert np.array_equal(kt, qkv[1].transpose(0, 2, 1))
+    assert np.array_equal(v, qkv[2])
+
+
+# ----------------------------------------------------------------------------------------- deform
+
+def _deform_inputs(shapes, b, q, h, d, p, seed, spread=0.5, softmax=True):
+    r = _rng(seed)
+    s = sum(hh * ww for hh, ww in shapes)
+    l = len(shapes)
+    value = r.standard_normal((b, s, h, d)).astype(np.float32)
+    loc = (r.standard_normal((b, q, h, l, p, 2)) * spread + 0.5).astype(np.float32)
+    logits = r.standard_normal((b, q, h, l * p))
+    attn = (refimpl.softmax64(logits) if softmax else logits).reshape(b, q, h, l, p).astype(np.float32)
+    return value, loc, attn
+
+
+DEFORM_CASES = [
+    ([(7, 9), (4, 5), (2, 3)], 1, 13, 4, 8, 3),  # tests/dino.rs:46-63
+    ([(9, 12), (5, 6), (3, 3), (2, 2)], 1, 37, 8, 32, 4),  # tests/kernels.rs:65-83
+    ([(5, 4), (3, 2)], 2, 6, 2, 4, 2),
+]
+
+
+@pytest.mark.parametrize("shapes,b,q,h,d,p", DEFORM_CASES)
+def test_deform_matches_scalar_spec_and_grid_sample(oracle_lib, shapes, b, q, h, d, p):
+    value, loc, attn = _deform_inputs(shapes, b, q, h, d, p, 9)
+    got = oracle_lib.deform_attn(value, loc, attn, shapes)
+    naive = refimpl.deform_naive64(value, loc, attn, shapes)
+    gs = refimpl.deform_grid_sample64(value, loc, attn, shapes)
+    assert np.abs(naive - gs).max() < 1e-12
+    assert np.abs(got - naive).max() < 1e-5
+
+
+def test_deform_pixel_centres_are_a_pure_gather(oracle_lib):
+    shapes = [(6, 8), (3, 4)]
+    b, q, h, d, p = 1, 5, 2, 4, 2
+    value, _, _ = _deform_inputs(shapes, b, q, h, d, p, 10)
+    r = _rng(11)
+    l = len(shapes)
+    loc = np.empty((b, q, h, l, p, 2), np.float32)
+    picks = np.empty((b, q, h, l, p, 2), np.int64)
+    for li, (hh, ww) in enumerate(shapes):
+        xs = r.integers(0, ww, size=(b, q, h, p))
+        ys = r.integers(0, hh, size=(b, q, h, p))
+        loc[:, :, :, li, :, 0] = (xs + 0.5) / ww
+        loc[:, :, :, li, :, 1] = (ys + 0.5) / hh
+        picks[:, :, :, li, :, 0] = xs
+        picks[:, :, :, li, :, 1] = ys
+    attn = np.zeros((b, q, h, l, p), np.float32)
+    attn[..., 1, 0] = 1.0  # one-hot on (level 1, point 0)
+    got = oracle_lib.deform_attn(value, loc, attn, shapes).reshape(b, q, h, d)
+    start = shapes[0][0] * shapes[0][1]
+    for qi in range(q):
+        for hi in range(h):
+            x, y = picks[0, qi, hi, 1, 0]
+            want = value[0, start + y * shapes[1][1] + x, hi]
+            np.testing.assert_allclose(got[0, qi, hi], want, rtol=1e-6, atol=1e-6)
+
+
+def test_deform_is_zero_beyond_one_pixel_outside(oracle_lib):
+    shapes = [(4, 4)]
+    value, loc, attn = _deform_inputs(shapes, 1, 3, 1, 4, 2, 12)
+    loc[..., 0] = -1.0 / 4  # x = -1.5 px: both corner columns are outside
+    got = oracle_lib.deform_attn(value, loc, attn, shapes)
+    assert np.all(got == 0)
+
+
+# ----------------------------------------------------------------------------------------- sdpa / flash
+
+@pytest.mark.parametrize("b,h,lq,lk,d", [(1, 1, 5, 7, 16), (2, 3, 33, 65, 64), (1, 1, 40, 100, 256)])
+def test_sdpa_matches_torch_float64(oracle_lib, b, h, lq, lk, d):
+    r = _rng(13)
+    q, k, v = (r.standard_normal((b, h, x, d)).astype(np.float32) for x in (lq, lk, lk))
+    got = oracle_lib.sdpa(q, k, v)
+    want = refimpl.sdpa64(q, k, v)
+    assert np.abs(got - want).max() < 2e-6
+
+
+def test_sdpa_closed_forms(oracle_lib):
+    r = _rng(14)
+    q = r.standard_normal((1, 1, 9, 32)).astype(np.float32)
+    v1 = r.standard_normal((1, 1, 1, 32)).astype(np.float32)
+    k1 = r.standard_normal((1, 1, 1, 32)).astype(np.float32)
+    np.testing.assert_allclose(oracle_lib.sdpa(q, k1, v1), np.broadcast_to(v1, q.shape), rtol=1e-6)
+    k = np.broadcast_to(k1, (1, 1, 20, 32)).copy()
+    v = r.standard_normal((1, 1, 20, 32)).astype(np.float32)
+    np.testing.assert_allclose(oracle_lib.sdpa(q, k, v), np.broadcast_to(v.mean(2, keepdims=True), q.shape),
+                               atol=1e-6)
+    k = r.standard_normal((1, 1, 20, 32)).astype(np.float32)
+    perm = r.permutation(20)
+    a = oracle_lib.sdpa(q, k, v)
+    b = oracle_lib.sdpa(q, k[:, :, perm], v[:, :, perm])
+    assert np.abs(a - b).max() < 1e-6
+
+
+@pytest.mark.parametrize("b,lq,lk,h,d", [(1, 5, 7, 2, 16), (2, 17, 9, 3, 64)])
+def test_mha_blhd_matches_torch(oracle_lib, b, lq, lk, h, d):
+    r = _rng(15)
+    q = r.standard_normal((b, lq, h, d)).astype(np.float32)
+    k = r.standard_normal((b, lk, h, d)).astype(np.float32)
+    v = r.standard_normal((b, lk, h, d)).astype(np.float32)
+    got = oracle_lib.mha_blhd(q, k, v)
+    want = refimpl.sdpa64(q.transpose(0, 2, 1, 3), k.transpose(0, 2, 1, 3), v.transpose(0, 2, 1, 3))
+    assert np.abs(got - want.transpose(0, 2, 1, 3)).max() < 2e-6
+
+
+# ----------------------------------------------------------------------------------------- rope
+
+@pytest.mark.parametrize("side,hd", [(4, 16), (64, 256), (9, 64)])
+def test_rope_tables_match_complex_form(oracle_lib, side, hd):
+    cos, sin = oracle_lib.rope_tables(side, 1.0, hd, 10000.0)
+    cis = refimpl.axial_rope_cis64(side, hd, 10000.0)
+    np.testing.assert_allclose(cos[:, 0::2], cis.real, atol=2e-5)
+    np.testing.assert_allclose(sin[:, 0::2], cis.imag, atol=2e-5)
+    assert np.array_equal(cos[:, 0::2], cos[:, 1::2]) and np.array_equal(sin[:, 0::2], sin[:, 1::2])
+    assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)  # angle zero at grid (0, 0)
+
+
+def test_rope_matches_complex_rotation_and_keeps_norms(oracle_lib):
+    side, hd = 8, 32
+    cos, sin = oracle_lib.rope_tables(side, 1.0, hd, 10000.0)
+    x = _rng(16).standard_normal((side * side, hd)).astype(np.float32)
+    got = oracle_lib.rope(x, cos, sin)
+    want = refimpl.rope_complex64(x, refimpl.axial_rope_cis64(side, hd, 10000.0))
+    assert np.abs(got - want).max() < 2e-5
+    n_in = x[:, 0::2] ** 2 + x[:, 1::2] ** 2
+    n_out = got[:, 0::2].astype(np.float64) ** 2 + got[:, 1::2] ** 2
+    np.testing.assert_allclose(n_out, n_in, rtol=2e-5, atol=1e-6)
+
+
+def test_rope_scores_depend_only_on_position_difference(oracle_lib):
+    side, hd = 8, 16
+    cos, sin = oracle_lib.rope_tables(side, 1.0, hd, 100.0)
+    r = _rng(17)
+    a, b = r.standard_normal(hd).astype(np.float32), r.standard_normal(hd).astype(np.float32)
+
+    def score(pa, pb):
+        ra = oracle_lib.rope(np.tile(a, (side * side, 1)), cos, sin)[pa]
+        rb = oracle_lib.rope(np.tile(b, (side * side, 1)), cos, sin)[pb]
+        return float(ra.astype(np.float64) @ rb)
+
+    # (row, col) (1,2)->(3,5) and (4,0)->(6,3): same offset (2, 3)
+    s1 = score(1 * side + 2, 3 * side + 5)
+    s2 = score(4 * side + 0, 6 * side + 3)
+    assert abs(s1 - s2) < 1e-4
+    assert abs(score(0, 1) - score(0, 2)) > 1e-3
+
+
+def test_rope_attention_matches_composed_float64(oracle_lib):
+    side, d, frames, n_excl = 4, 32, 3, 4
+    cos, sin = oracle_lib.rope_tables(side, 1.0, d, 10000.0)
+    lq, mk = side * side, frames * side * side + n_excl
+    r = _rng(18)
+    q = r.standard_normal((lq, d)).astype(np.float32)
+    k = r.standard_normal((mk, d)).astype(np.float32)
+    v = r.standard_normal((mk, d)).astype(np.float32)
+    got = oracle_lib.rope_attention(q, k, v, cos, sin, n_excl)
+    cis = refimpl.axial_rope_cis64(side, d, 10000.0)
+    qr = refimpl.rope_complex64(q, cis)
+    kr = np.concatenate([refimpl.rope_complex64(k[: mk - n_excl], np.tile(cis, (frames, 1))),
+                         k[mk - n_excl:].astype(np.float64)])
+    want = refimpl.sdpa64(qr, kr, v)
+    assert np.abs(got - want).max() < 5e-5
+
+
+# ----------------------------------------------------------------------------------------- helpers
+
+def test_rounding_helpers_are_round_to_nearest_even(oracle_lib):
+    import torch
+
+    x = np.concatenate([_rng(19).standard_normal(10000).astype(np.float32) * 100,
+                        np.array([65504, 65519, 65520, 1e-8, -3e-5, 0.0, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11],
+                                 np.float32)])
+    assert np.array_equal(oracle_lib.round_to(x, "f16"), x.astype(np.float16).astype(np.float32))
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    assert np.array_equal(oracle_lib.round_to(x, "bf16"), want)
+
+
+def test_randn_is_seeded_and_normal(oracle_lib):
+    a = oracle_lib.randn(7, (100000,))
+    b = oracle_lib.randn(7, (100000,))
+    c = oracle_lib.randn(8, (100000,))
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    assert abs(a.mean()) < 0.02 and abs(a.std() - 1) < 0.02
