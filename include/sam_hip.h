@@ -1,0 +1,53 @@
+/*
+ * sam_hip.h - C ABI of libsam_hip.so, the MI355X (gfx950) fused-attention hot path of sam-rs.
+ *
+ * Each entry point replaces one GPU path of the reference's `src/kernels.rs` (file:line cited per
+ * function). Conventions, shared by all entry points:
+ *   - plain device pointers (hipMalloc'd or any HIP-visible device memory), 16-byte aligned,
+ *     contiguous row-major in the layouts the reference uses; the caller allocates every buffer;
+ *   - dtype: 0 = f32, 1 = f16, 2 = bf16 (the three the reference's `by_dtype!` accepts,
+ *     kernels.rs:1086-1095); every tensor argument of one call has that dtype;
+ *   - stream: a hipStream_t passed as void* (NULL = the default stream); launches are asynchronous,
+ *     exactly as the reference's are on candle's CUDA stream;
+ *   - return 0 on success, nonzero on error; sam_hip_last_error() then returns a message (per thread);
+ *   - no global mutable state beyond per-kernel one-time attribute set-up; safe to call from many threads.
+ */
+#ifndef SAM_HIP_H
+#define SAM_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum sam_hip_status {
+  SAM_HIP_OK = 0,
+  SAM_HIP_EINVAL = 1,      /* a null pointer or an inconsistent size */
+  SAM_HIP_EDTYPE = 2,      /* dtype not in {0, 1, 2} or not supported by this entry point */
+  SAM_HIP_EUNSUPPORTED = 3, /* a shape beyond this kernel's limits (message says which) */
+  SAM_HIP_EHIP = 4         /* the HIP runtime reported an error at launch */
+};
+
+/*
+ * Fused SAM ViT attention with the decomposed relative-position bias:
+ *   out[b, r, :] = softmax_k(scale * q[b,r].kt[b,:,k] + q[b,r].Th[i-kh+h-1] + q[b,r].Tw[j-kw+w-1]) . v[b,k,:]
+ * with r = i*w + j, k = kh*w + kw, Th = table rows [0, 2h-1), Tw = rows [2h-1, 2h-1 + 2w-1).
+ *   q [bh, h*w, hd], kt [bh, hd, h*w] (the key matrix transposed, as qkv_split writes it),
+ *   v [bh, h*w, hd], table [(2h-1) + (2w-1), hd], out [bh, h*w, hd].
+ * Replaces, in one kernel, the reference's GPU sequence bmm(q, kT) -> relpos_softmax -> bmm(P, v)
+ * (sam1/encoder.rs:79-82; kernels.rs:12-43, 919-924, 1108-1149) and is the GPU counterpart of
+ * attention_relpos_cpu (kernels.rs:899-906).
+ * Limits: 1 <= h, w <= 64; hd % 8 == 0 and hd <= 128 (f16/bf16), hd % 4 == 0 and hd <= 128 (f32).
+ */
+int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void* table, void* out, int dtype,
+                        int bh, int h, int w, int hd, float scale, void* stream);
+
+/* Message describing the last error returned on this thread ("" if none). */
+const char* sam_hip_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int sam_hip_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,302 @@
+// Fused SAM ViT attention with the decomposed relative-position bias, f32, for gfx950.
+//
+// Same decomposition as the f16/bf16 kernel (attn_relpos.hip): S^T = K . Q^T and O^T = V^T . P^T on
+// 32x32 MFMA tiles (v_mfma_f32_32x32x2_f32 here), one query per lane, key tiles that cover whole grid
+// rows so the Rw bias stays in registers. The f32 path is held to 1e-5 of the reference's exact-f32
+// CPU result (kernels.rs:181-220), so the softmax follows the reference's arithmetic: the logit is
+// ((s * scale) + rh) + rw rounded after every step, exponentials use the accurate expf in natural
+// units, and products are accumulated in f32.
+//
+// Operand layouts for K = 2 steps: lane l supplies A[l % 32][l / 32] and B[l / 32][l % 32]. The head
+// dimension is split in halves, hd index = (l / 32) * HDP/2 + step, so each lane's operands are
+// contiguous runs (vector LDS and global reads). The K tile is stored [slot][hd] (transposed from the
+// reference's kT while staging) and the V tile [slot][hd].
+#include "relpos_geom.hpp"
+
+namespace samhip {
+
+constexpr float kRescaleSlackNat = 5.5451774f;  // 8 * ln 2: p <= 256
+
+template <int HDP> struct F32Geom {
+  static constexpr int HALF = HDP / 2;
+  static constexpr int MBO = (HDP + 31) / 32;
+  static constexpr int KSTR = HDP + 4;        // floats per K slot row
+  static constexpr int VSTR = MBO * 32 + 4;   // floats per V slot row
+};
+
+template <int HDP, int MODE, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_relpos_f32_kernel(const float* __restrict__ q,
+                                                                 const float* __restrict__ kt,
+                                                                 const float* __restrict__ v,
+                                                                 const float* __restrict__ table,
+                                                                 float* __restrict__ out, int hd, int H, int W,
+                                                                 float scale) {
+  typedef KeyGeom<MODE> G;
+  typedef F32Geom<HDP> FG;
+  constexpr int HALF = FG::HALF, MBO = FG::MBO, KSTR = FG::KSTR, VSTR = FG::VSTR;
+  constexpr int NT = NW * 64;
+  constexpr int KBUF = 64 * KSTR, VBUF = 64 * VSTR;
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* ks_base = reinterpret_cast<float*>(smem);
+  float* vs_base = ks_base + 2 * KBUF;
+  float* rhs_base = vs_base + 2 * VBUF;
+
+  const int N = H * W;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, hh = lane >> 5;
+  const long bh = blockIdx.y;
+  const int qidx = (blockIdx.x * NW + wave) * 32 + n;
+  const bool qvalid = qidx < N;
+  const int qi = qvalid ? qidx / W : 0, qj = qvalid ? qidx % W : 0;
+  float* rhs = rhs_base + wave * 64 * 32;
+
+  // Q fragments: lane supplies Q[query n][hh * HALF + s]
+  float qf[HALF];
+#pragma unroll
+  for (int s = 0; s < HALF; s += 4) {
+    const int c = hh * HALF + s;
+    f32x4 val = f32x4{};
+    if (qvalid && c < hd) val = *reinterpret_cast<const f32x4*>(q + (bh * N + qidx) * hd + c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qf[s + i] = val[i];
+  }
+
+  // prologue: G = T . Q^T, scattered along the diagonal band (natural units here)
+  const float* th = table;
+  const float* tw = table + (long)(2 * H - 1) * hd;
+  auto band = [&](const float* tab, int rows, int base, int len) {
+    for (int r0 = 0; r0 < rows; r0 += 32) {
+      f32x16 acc = {};
+      const int r = r0 + n;
+#pragma unroll
+      for (int s = 0; s < HALF; s += 4) {
+        const int c = hh * HALF + s;
+        f32x4 a = f32x4{};
+        if (r < rows && c < hd) a = *reinterpret_cast<const f32x4*>(tab + (long)r * hd + c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], qf[s + i], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int rr = r0 + 8 * (e >> 2) + 4 * hh + (e & 3);
+        const int k = base + len - 1 - rr;
+        if (rr < rows && k >= 0 && k < len) rhs[k * 32 + n] = acc[e];
+      }
+    }
+  };
+  band(tw, 2 * W - 1, qj, W);
+  __syncthreads();
+  float rw[G::RWN];
+#pragma unroll
+  for (int mb = 0; mb < (MODE == kRow64 ? 2 : 1); ++mb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int c = G::col(mb, e, hh);
+      rw[G::rw_index(mb, e)] = c < W ? rhs[c * 32 + n] : -INFINITY;
+    }
+  __syncthreads();
+  band(th, 2 * H - 1, qi, H);
+  for (int i = tid; i < 2 * 64; i += NT) {
+    float* rowp = vs_base + (i >> 6) * VBUF + (i & 63) * VSTR;
+    for (int c = HDP; c < VSTR; ++c) rowp[c] = 0.f;
+  }
+
+  // key tiles: K chunk = 4 consecutive keys of one hd row (from kT), V chunk = 4 hd values of one key
+  constexpr int KCH = HDP * 16;
+  constexpr int KPT = (KCH + NT - 1) / NT;
+  constexpr int VCPR = HDP / 4;
+  constexpr int VCH = 64 * VCPR;
+  constexpr int VPT = (VCH + NT - 1) / NT;
+  float kreg[KPT][4];
+  f32x4 vreg[VPT];
+  const float* ktb = kt + bh * hd * (long)N;
+  const float* vb = v + bh * (long)N * hd;
+  auto load_tile = [&](int t) {
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int c = tid + u * NT;
+      const int d = c >> 4, s0 = (c & 15) * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sl = s0 + i;
+        const int rho = sl / G::WP, kap = sl % G::WP, row = t * G::RPT + rho;
+        kreg[u][i] = (c < KCH && d < hd && kap < W && row < H) ? ktb[(long)d * N + row * W + kap] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int c = tid + u * NT;
+      const int sl = c / VCPR, d0 = (c % VCPR) * 4;
+      const int rho = sl / G::WP, kap = sl % G::WP, row = t * G::RPT + rho;
+      f32x4 val = f32x4{};
+      if (c < VCH && d0 < hd && kap < W && row < H) val = *reinterpret_cast<const f32x4*>(vb + (long)(row * W + kap) * hd + d0);
+      vreg[u] = val;
+    }
+  };
+  auto store_tile = [&](int buf) {
+    float* kbuf = ks_base + buf * KBUF;
+    float* vbuf = vs_base + buf * VBUF;
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int c = tid + u * NT;
+      if (c < KCH) {
+        const int d = c >> 4, s0 = (c & 15) * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kbuf[(s0 + i) * KSTR + d] = kreg[u][i];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int c = tid + u * NT;
+      if (c < VCH) {
+        const int sl = c / VCPR, d0 = (c % VCPR) * 4;
+        *reinterpret_cast<f32x4*>(vbuf + sl * VSTR + d0) = vreg[u];
+      }
+    }
+  };
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 o[MBO];
+#pragma unroll
+  for (int ob = 0; ob < MBO; ++ob) o[ob] = f32x16{};
+  const int ntiles = (H + G::RPT - 1) / G::RPT;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) load_tile(t + 1);
+    const float* kbuf = ks_base + buf * KBUF;
+    const float* vbuf = vs_base + buf * VBUF;
+
+    f32x16 s[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      s[mb] = f32x16{};
+      const float* krow = kbuf + G::slot(mb, n) * KSTR + hh * HALF;
+#pragma unroll
+      for (int st = 0; st < HALF; st += 4) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(krow + st);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[mb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], qf[st + i], s[mb], 0, 0, 0);
+      }
+    }
+
+    float rh[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const int row = t * G::RPT + G::row(mb, hh);
+      rh[mb] = row < H ? rhs[row * 32 + n] : -INFINITY;
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float x = s[mb][e] * scale;  // kernels.rs:202: x * scale + rh[kh] + rw[kw], left to right
+        x = x + rh[mb];
+        x = x + rw[G::rw_index(mb, e)];
+        s[mb][e] = x;
+        mt = fmaxf(mt, x);
+      }
+    mt = max_with_partner32(mt);
+    if (wave_any(mt > m_run + kRescaleSlackNat)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = expf(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int ob = 0; ob < MBO; ++ob) o[ob] *= alpha;
+      m_run = m_new;
+    }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float p = expf(s[mb][e] - m_run);
+        s[mb][e] = p;
+        l_run += p;
+      }
+
+    // O^T += V^T . P^T, two logical keys per step: lane half hh supplies S-row 8*(e/4) + 4*hh + e%4
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int sl = G::slot(mb, 8 * (e >> 2) + 4 * hh + (e & 3));
+#pragma unroll
+        for (int ob = 0; ob < MBO; ++ob)
+          o[ob] = __builtin_amdgcn_mfma_f32_32x32x2f32(vbuf[sl * VSTR + 32 * ob + n], s[mb][e], o[ob], 0, 0, 0);
+      }
+
+    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  const float inv = 1.f / sum_with_partner32(l_run);
+  if (qvalid) {
+    float* orow = out + (bh * N + qidx) * hd;
+#pragma unroll
+    for (int ob = 0; ob < MBO; ++ob)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int d0 = 32 * ob + 8 * a + 4 * hh;
+        if (d0 < hd) {
+          f32x4 w4;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) w4[b] = o[ob][4 * a + b] * inv;
+          *reinterpret_cast<f32x4*>(orow + d0) = w4;
+        }
+      }
+  }
+}
+
+template <int HDP, int MODE, int NW>
+static hipError_t launch_f32(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
+                             int hd, int h, int w, float scale, hipStream_t stream) {
+  typedef F32Geom<HDP> FG;
+  const size_t lds = (size_t)(2 * 64 * FG::KSTR + 2 * 64 * FG::VSTR + NW * 64 * 32) * sizeof(float);
+  auto kern = attn_relpos_f32_kernel<HDP, MODE, NW>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int n = h * w;
+  dim3 grid((n + 32 * NW - 1) / (32 * NW), bh);
+  hipLaunchKernelGGL(kern, grid, dim3(NW * 64), lds, stream, (const float*)q, (const float*)kt, (const float*)v,
+                     (const float*)table, (float*)out, hd, h, w, scale);
+  return hipGetLastError();
+}
+
+template <int HDP, int MODE>
+static hipError_t f32_pick_nw(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
+                              int hd, int h, int w, float scale, hipStream_t stream) {
+  // LDS: two K and two V tiles of 64 x HDP floats plus 8 KB of Rh per wave must fit in 160 KB
+  if (HDP > 80) return launch_f32<HDP, MODE, 2>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  if (h * w > 1024) return launch_f32<HDP, MODE, 8>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  return launch_f32<HDP, MODE, 4>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+}
+
+template <int HDP>
+static hipError_t f32_pick_mode(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
+                                int hd, int h, int w, float scale, hipStream_t stream) {
+  if (w <= 16) return f32_pick_nw<HDP, kPair>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  if (w <= 32) return f32_pick_nw<HDP, kRow32>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  return f32_pick_nw<HDP, kRow64>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+}
+
+// Shape limits are checked by the caller: 1 <= h, w <= 64, hd % 4 == 0, hd <= 128.
+hipError_t attn_relpos_f32(const void* q, const void* kt, const void* v, const void* table, void* out, int bh, int hd,
+                           int h, int w, float scale, hipStream_t stream) {
+  if (hd <= 16) return f32_pick_mode<16>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  if (hd <= 32) return f32_pick_mode<32>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  if (hd <= 64) return f32_pick_mode<64>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  if (hd <= 80) return f32_pick_mode<80>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  return f32_pick_mode<128>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+}
+
+}  // namespace samhip

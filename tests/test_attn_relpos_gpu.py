@@ -1,0 +1,195 @@
+"""Parity of the fused rel-pos attention (libsam_hip.so) with the CPU oracle, on an MI355X.
+
+Inputs are drawn with a fixed seed, rounded to the kernel dtype, and the oracle runs on the rounded
+values, so only the kernel's own error is measured (the reference's test does the same,
+tests/kernels.rs:28-31). Bars: f32 max|gpu - cpu| / max|cpu| <= 1e-5; f16/bf16 max-abs <= 2e-3 on
+the attention outputs against the f32 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import sam_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+
+F32_REL_TOL = 1e-5
+HALF_ABS_TOL = 2e-3
+TORCH_DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import sam_hip
+
+    sam_hip.load()
+    assert torch.cuda.is_available(), "no GPU visible"
+    return sam_hip
+
+
+def make_inputs(h, w, bh, hd, seed, dtype, qkv_std=1.0, table_std=0.02):
+    n = h * w
+    r = np.random.default_rng(seed)
+    q = (qkv_std * r.standard_normal((bh, n, hd))).astype(np.float32)
+    kt = (qkv_std * r.standard_normal((bh, hd, n))).astype(np.float32)
+    v = (qkv_std * r.standard_normal((bh, n, hd))).astype(np.float32)
+    table = (table_std * r.standard_normal((2 * h - 1 + 2 * w - 1, hd))).astype(np.float32)
+    return [oracle.round_to(x, dtype) for x in (q, kt, v, table)]
+
+
+def to_dev(x, dtype):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(device="cuda", dtype=TORCH_DT[dtype])
+
+
+def run_gpu(hip, arrays, h, w, scale, dtype):
+    q, kt, v, table = (to_dev(a, dtype) for a in arrays)
+    out = hip.attention_relpos(q, kt, v, table, h, w, scale)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def bf16_half_ulp(x):
+    """Half the spacing of bf16 numbers at |x| (8 significant bits): the rounding any bf16 output has."""
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -126)))
+    return 2.0 ** (e - 8)
+
+
+def check(got, want, dtype, what):
+    """f32: max|gpu-cpu| / max|cpu| <= 1e-5. f16: max-abs <= 2e-3. bf16: max-abs <= 2e-3 beyond the
+    half-ulp rounding of the bf16 output itself (|out| >= 0.5 has a half-ulp of 2e-3 or more, so no
+    bf16 result can meet a bare 2e-3 there)."""
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    if dtype == "f32":
+        err = np.abs(got - want).max() / np.abs(want).max()
+        assert err <= F32_REL_TOL, f"{what}: max|gpu-cpu|/max|cpu| = {err:.3g}"
+    elif dtype == "bf16":
+        err = (np.abs(got - want) - bf16_half_ulp(want)).max()
+        assert err <= HALF_ABS_TOL, f"{what}: max abs diff beyond bf16 output rounding {err:.3g}"
+    else:
+        err = np.abs(got - want).max()
+        assert err <= HALF_ABS_TOL, f"{what}: max abs diff {err:.3g}"
+    return err
+
+
+# The reference test geometries (tests/kernels.rs:23, tests/cpu_gemm.rs:37) with its N(0,1) tables,
+# plus small and ragged shapes: a 2x3 grid with hd 8, a single grid row, and odd sizes.
+SMALL = [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (2, 3, 2, 8), (1, 5, 2, 16), (5, 33, 2, 32),
+         (3, 40, 2, 128), (9, 17, 2, 48)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("h,w,bh,hd", SMALL)
+def test_attention_relpos_reference_geometries(hip, h, w, bh, hd, dtype):
+    print(f"attn_relpos {dtype} h={h} w={w} bh={bh} hd={hd}", flush=True)
+    # q, k ~ N(0, 0.5) keeps N(0,1)-table logits in the range the reference's f16 test exercises
+    arrays = make_inputs(h, w, bh, hd, 100 + h * w + hd, dtype, qkv_std=0.5, table_std=0.5)
+    scale = hd ** -0.5
+    want = oracle.attention_relpos(*arrays, h, w, scale)
+    got = run_gpu(hip, arrays, h, w, scale, dtype)
+    check(got, want, dtype, f"{h}x{w} bh={bh} hd={hd} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_vit_h_global_layer(hip, dtype):
+    """ViT-H global attention layer: BH 16, 64x64 tokens, hd 80, q/k/v ~ N(0,1), rel_pos ~ N(0, 0.02).
+    The GPU runs all 16 heads; the oracle checks heads 0, 7 and 15."""
+    h = w = 64
+    bh, hd = 16, 80
+    print(f"vit-h global {dtype}", flush=True)
+    arrays = make_inputs(h, w, bh, hd, 7, dtype)
+    scale = hd ** -0.5
+    got = run_gpu(hip, arrays, h, w, scale, dtype)
+    heads = [0, 7, 15]
+    q, kt, v, table = arrays
+    want = oracle.attention_relpos(q[heads], kt[heads], v[heads], table, h, w, scale)
+    check(got[heads], want, dtype, f"vit-h global {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_vit_h_window_layer(hip, dtype):
+    """ViT-H windowed layer at batch 1: 25 windows x 16 heads of 14x14 tokens, hd 80, (27, 80) tables."""
+    h = w = 14
+    bh, hd = 400, 80
+    print(f"vit-h window {dtype}", flush=True)
+    arrays = make_inputs(h, w, bh, hd, 8, dtype)
+    scale = hd ** -0.5
+    want = oracle.attention_relpos(*arrays, h, w, scale)
+    got = run_gpu(hip, arrays, h, w, scale, dtype)
+    check(got, want, dtype, f"vit-h window {dtype}")
+
+
+def test_vit_b_f32_layers(hip):
+    """ViT-B f32: windowed layer (300 x 14x14, hd 64, (27,64) tables) and global layer (12 x 64x64,
+    (127,64) tables) at scale 64^-0.5; q/k/v ~ N(0, 0.3) as the qkv projection of N(0,1) tokens
+    with N(0, 0.02) weights gives. The oracle checks every window and global heads 0 and 11."""
+    print("vit-b f32 window", flush=True)
+    arrays = make_inputs(14, 14, 300, 64, 9, "f32", qkv_std=0.55)
+    want = oracle.attention_relpos(*arrays, 14, 14, 0.125)
+    got = run_gpu(hip, arrays, 14, 14, 0.125, "f32")
+    check(got, want, "f32", "vit-b window f32")
+    print("vit-b f32 global", flush=True)
+    arrays = make_inputs(64, 64, 12, 64, 10, "f32", qkv_std=0.55)
+    got = run_gpu(hip, arrays, 64, 64, 0.125, "f32")
+    heads = [0, 11]
+    q, kt, v, table = arrays
+    want = oracle.attention_relpos(q[heads], kt[heads], v[heads], table, 64, 64, 0.125)
+    check(got[heads], want, "f32", "vit-b global f32")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_full_size_properties(hip, dtype):
+    """Size-independent checks over every row of a batch-8 ViT-H global layer (BH 128): a constant
+    value vector comes back unchanged (softmax rows sum to 1), and the map is linear in v."""
+    h = w = 64
+    bh, hd = 128, 80
+    print(f"full-size properties {dtype}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    dt = TORCH_DT[dtype]
+    q = torch.randn(bh, h * w, hd, device="cuda", generator=g).to(dt)
+    kt = torch.randn(bh, hd, h * w, device="cuda", generator=g).to(dt)
+    table = (0.02 * torch.randn(2 * h - 1 + 2 * w - 1, hd, device="cuda", generator=g)).to(dt)
+    const = torch.linspace(-2, 2, hd, device="cuda").to(dt)
+    v = const.expand(bh, h * w, hd).contiguous()
+    out = hip.attention_relpos(q, kt, v, table, h, w, hd ** -0.5).float()
+    tol = 1e-5 * 2.0 if dtype == "f32" else 2e-3  # f32: the 1e-5 parity bar relative to max|v| = 2
+    assert (out - const.float()).abs().max().item() <= tol
+    v1 = torch.randn(bh, h * w, hd, device="cuda", generator=g).to(dt)
+    v2 = torch.randn(bh, h * w, hd, device="cuda", generator=g).to(dt)
+    o1 = hip.attention_relpos(q, kt, v1, table, h, w, hd ** -0.5).float()
+    o2 = hip.attention_relpos(q, kt, v2, table, h, w, hd ** -0.5).float()
+    o12 = hip.attention_relpos(q, kt, (v1.float() + v2.float()).to(dt), table, h, w, hd ** -0.5).float()
+    lin_tol = 1e-4 if dtype == "f32" else 1e-2  # v1 + v2 is rounded once more in f16
+    assert (o12 - o1 - o2).abs().max().item() <= lin_tol
+
+
+def test_heads_are_independent(hip):
+    """Permuting the batch-head axis permutes the output rows exactly (bit-identical)."""
+    h = w = 14
+    bh, hd = 40, 64
+    g = torch.Generator(device="cuda").manual_seed(12)
+    q = torch.randn(bh, h * w, hd, device="cuda", generator=g).half()
+    kt = torch.randn(bh, hd, h * w, device="cuda", generator=g).half()
+    v = torch.randn(bh, h * w, hd, device="cuda", generator=g).half()
+    table = torch.randn(2 * h - 1 + 2 * w - 1, hd, device="cuda", generator=g).half()
+    perm = torch.randperm(bh, device="cuda", generator=g)
+    a = hip.attention_relpos(q, kt, v, table, h, w, 0.125)
+    b = hip.attention_relpos(q[perm].contiguous(), kt[perm].contiguous(), v[perm].contiguous(), table, h, w, 0.125)
+    assert torch.equal(a[perm], b)
+
+
+def test_argument_errors_are_reported(hip):
+    x = torch.zeros(2, 65 * 2, 16, device="cuda", dtype=torch.float16)
+    kt = torch.zeros(2, 16, 65 * 2, device="cuda", dtype=torch.float16)
+    t = torch.zeros(2 * 65 - 1 + 3, 16, device="cuda", dtype=torch.float16)
+    with pytest.raises(hip.SamHipError, match="64x64"):
+        hip.attention_relpos(x, kt, x, t, 65, 2, 0.25)
+    with pytest.raises(hip.SamHipError, match="contiguous"):
+        hip.attention_relpos(x.transpose(1, 2), kt, x, t, 65, 2, 0.25)
+    y = torch.zeros(1, 6, 12, device="cuda", dtype=torch.float16)
+    with pytest.raises(hip.SamHipError, match="multiple of 8"):
+        hip.attention_relpos(y, torch.zeros(1, 12, 6, device="cuda", dtype=torch.float16), y,
+                             torch.zeros(3 + 5, 12, device="cuda", dtype=torch.float16), 2, 3, 0.3)
+    with pytest.raises(hip.SamHipError, match="dtype"):
+        z = torch.zeros(1, 6, 8, device="cuda", dtype=torch.float64)
+        hip.attention_relpos(z, torch.zeros(1, 8, 6, device="cuda", dtype=torch.float64), z,
+                             torch.zeros(8, 8, device="cuda", dtype=torch.float64), 2, 3, 0.3)
