@@ -36,6 +36,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--dtype", default="f16", choices=["f16", "bf16"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layers", default="all", choices=["all", "global", "window"],
+                    help="restrict the step to one layer kind (for profiling one kernel)")
     return ap.parse_args()
 
 
@@ -134,8 +136,13 @@ def main():
         if rc:
             raise sam_hip.SamHipError(lib.sam_hip_last_error().decode())
 
+    keep = {"all": lambda i: True, "global": lambda i: i in GLOBAL_LAYERS,
+            "window": lambda i: i not in GLOBAL_LAYERS}[args.layers]
+
     def step(ev=None):
         for i, L in enumerate(layers):
+            if not keep(i):
+                continue
             if ev is not None and i in GLOBAL_LAYERS:
                 ev[0].append(torch.cuda.Event(enable_timing=True))
                 ev[1].append(torch.cuda.Event(enable_timing=True))
@@ -163,8 +170,12 @@ def main():
     torch.cuda.synchronize()
     ms_total = t0e.elapsed_time(t1e)
     ms_step = ms_total / args.steps
-    glob_ms = sum(a.elapsed_time(b) for a, b in zip(evs[0], evs[1])) / len(evs[0])
-    win_ms = sum(a.elapsed_time(b) for a, b in zip(evs[2], evs[3])) / len(evs[2])
+    glob_ms = sum(a.elapsed_time(b) for a, b in zip(evs[0], evs[1])) / max(len(evs[0]), 1)
+    win_ms = sum(a.elapsed_time(b) for a, b in zip(evs[2], evs[3])) / max(len(evs[2]), 1)
+    if args.layers != "all":
+        print(json.dumps({"layers": args.layers, "ms_per_step": ms_step, "global_layer_us": glob_ms * 1e3,
+                          "window_layer_us": win_ms * 1e3}), flush=True)
+        return
 
     gbh, wbh = args.batch * HEADS, args.batch * WINDOWS * HEADS
     g_flops = flops(gbh, 4096)
