@@ -41,6 +41,40 @@ enum sam_hip_status {
 int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void* table, void* out, int dtype,
                         int bh, int h, int w, int hd, float scale, void* stream);
 
+/*
+ * Softmax over materialised scores with the decomposed relative-position bias:
+ *   out[b, r, k] = softmax_k(scale * s[b, r, k] + q[b,r].Th[i-kh+h-1] + q[b,r].Tw[j-kw+w-1])
+ *   s [bh, h*w, h*w], q [bh, h*w, hd], table as above -> out [bh, h*w, h*w]; rows = bh*h*w.
+ * The literal drop-in for kernels::relpos_softmax (kernels.rs:12-43; GPU op kernels.rs:1108-1149,
+ * sam.cu:44-96) for callers that hold the score matrix. Limits: h*w <= 8192 (the reference's GPU
+ * limit, kernels.rs:1078-1083), h, w <= 128, hd <= 256.
+ */
+int sam_hip_relpos_softmax(const void* s, const void* q, const void* table, void* out, int dtype, long rows, int h,
+                           int w, int hd, float scale, void* stream);
+
+/*
+ * qkv projection output to the attention layout, bias added:
+ *   y [tokens, 3*nh*hd] (columns (qkv, head, d)), bias [3*nh*hd] -> out [3, bh*n*hd] holding
+ *   q [bh, n, hd], kT [bh, hd, n], v [bh, n, hd] back to back, bh = tokens/n * nh.
+ * Replaces kernels::qkv_split (kernels.rs:872-894; GPU op sam.cu:111-128). Each element is
+ * round(y + bias) as the reference computes it. Limits: tokens % n == 0, hd <= 256.
+ */
+int sam_hip_qkv_split(const void* y, const void* bias, void* out, int dtype, long tokens, int n, int nh, int hd,
+                      void* stream);
+
+/*
+ * Multi-scale deformable attention (Grounding DINO), forward:
+ *   out[b, q, h*d + c] = sum_{l,p} attn[b,q,h,l,p] * bilinear(value_l[b,:,h,c], (x*W_l - 0.5, y*H_l - 0.5))
+ * with (x, y) = loc[b,q,h,l,p,:], zero padding outside each level.
+ *   value [b, s, h, d] (levels concatenated), loc [b, q, h, l, p, 2], attn [b, q, h, l, p] -> out [b, q, h*d].
+ *   shapes: host array of 2*l ints, (height, width) of each level; their pixels must add up to s.
+ * Replaces kernels::deform_attn (kernels.rs:824-835) on the GPU (cuda::DeformAttn, kernels.rs:1162-1194;
+ * sam.cu:305-350). Limits: l <= 4 (the reference's GPU error, kernels.rs:1175-1177), l*p <= 64,
+ * b*s*h*d < 2^31.
+ */
+int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, void* out, int dtype, int b, int s,
+                        int q, int h, int d, int l, int p, const int* shapes, void* stream);
+
 /* Message describing the last error returned on this thread ("" if none). */
 const char* sam_hip_last_error(void);
 

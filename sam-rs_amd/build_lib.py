@@ -21,6 +21,9 @@ LIB = os.path.join(HERE, "libsam_hip.so")
 SOURCES = [
     "attn_relpos.hip",
     "attn_relpos_f32.hip",
+    "deform_attn.hip",
+    "relpos_softmax.hip",
+    "qkv_split.hip",
     "sam_hip_abi.cpp",
 ]
 

@@ -32,6 +32,10 @@ template <> struct Vec<bf16> {
   typedef bf16x8 x8;
   typedef bf16x4 x4;
 };
+template <> struct Vec<float> {
+  typedef float x8 __attribute__((ext_vector_type(8)));
+  typedef f32x4 x4;
+};
 
 __device__ __forceinline__ float to_f32(float v) { return v; }
 __device__ __forceinline__ float to_f32(f16 v) { return (float)v; }

@@ -1,0 +1,115 @@
+"""Parity of the multi-scale deformable attention (libsam_hip.so) with the CPU oracle, on an MI355X.
+
+Cases: the reference's own test shapes (tests/kernels.rs:65-83, tests/dino.rs:46-63) with sampling
+locations spread beyond [0, 1] so the zero padding is exercised, plus the Grounding DINO-tiny encoder and
+decoder layers at full size. Bars: f32 max-abs 1e-4 (the reference test's, tests/kernels.rs:78); f16
+and bf16 max-abs against the f32 oracle on the same rounded inputs: 2e-3 (f16) and the reference
+test's 5e-2 (bf16, whose 8-bit inputs and output cannot do better on values ~N(0,1)).
+"""
+import numpy as np
+import pytest
+import torch
+
+import sam_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+TORCH_DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+TOL = {"f32": 1e-4, "f16": 2e-3, "bf16": 5e-2}
+
+DINO_LEVELS = [(100, 167), (50, 84), (25, 42), (13, 21)]
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import sam_hip
+
+    sam_hip.load()
+    assert torch.cuda.is_available(), "no GPU visible"
+    return sam_hip
+
+
+def inputs(shapes, b, q, h, d, p, seed, spread=0.5, dtype="f32"):
+    r = np.random.default_rng(seed)
+    s = sum(hh * ww for hh, ww in shapes)
+    l = len(shapes)
+    value = r.standard_normal((b, s, h, d)).astype(np.float32)
+    loc = (r.standard_normal((b, q, h, l, p, 2)) * spread + 0.5).astype(np.float32)
+    logits = r.standard_normal((b, q, h, l * p))
+    attn = np.exp(logits - logits.max(-1, keepdims=True))
+    attn = (attn / attn.sum(-1, keepdims=True)).reshape(b, q, h, l, p).astype(np.float32)
+    return [oracle.round_to(x, dtype) for x in (value, loc, attn)]
+
+
+def run(hip, arrays, shapes, dtype):
+    dev = [torch.from_numpy(a).to("cuda", TORCH_DT[dtype]) for a in arrays]
+    out = hip.deform_attn(*dev, shapes)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+CASES = [
+    ("kernels.rs", [(9, 12), (5, 6), (3, 3), (2, 2)], 1, 37, 8, 32, 4, 0.5),
+    ("dino.rs", [(7, 9), (4, 5), (2, 3)], 1, 13, 4, 8, 3, 0.6),
+    ("batch2-odd-d", [(6, 5), (3, 3)], 2, 11, 3, 20, 2, 0.7),
+    ("single-level", [(16, 16)], 1, 64, 2, 64, 8, 0.4),
+    ("d-not-multiple-of-4", [(5, 7), (2, 4)], 1, 9, 2, 6, 3, 0.5),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("name,shapes,b,q,h,d,p,spread", CASES, ids=[c[0] for c in CASES])
+def test_deform_matches_oracle(hip, name, shapes, b, q, h, d, p, spread, dtype):
+    print(f"deform {name} {dtype}", flush=True)
+    arrays = inputs(shapes, b, q, h, d, p, 20 + q, spread, dtype)
+    want = oracle.deform_attn(*arrays, shapes)
+    got = run(hip, arrays, shapes, dtype)
+    err = np.abs(got - want).max()
+    assert np.isfinite(got).all() and err <= TOL[dtype], f"{name} {dtype}: max abs diff {err:.3g}"
+
+
+@pytest.mark.parametrize("q", [22223, 900], ids=["encoder", "decoder"])
+def test_dino_tiny_full_size(hip, q):
+    """Grounding DINO-tiny: 800x1333 input -> 4 levels, 22223 value tokens, 8 heads x 32, 4 points."""
+    print(f"deform dino-tiny q={q}", flush=True)
+    r = np.random.default_rng(q)
+    s = sum(a * b for a, b in DINO_LEVELS)
+    value = r.standard_normal((1, s, 8, 32)).astype(np.float32)
+    ref = r.uniform(0, 1, (1, q, 1, 1, 1, 2))
+    wh = np.array([[w, h] for h, w in DINO_LEVELS], np.float64).reshape(1, 1, 1, 4, 1, 2)
+    loc = (ref + r.normal(0, 2, (1, q, 8, 4, 4, 2)) / wh).astype(np.float32)  # offsets ~N(0,2) px
+    logits = r.standard_normal((1, q, 8, 16))
+    attn = np.exp(logits - logits.max(-1, keepdims=True))
+    attn = (attn / attn.sum(-1, keepdims=True)).reshape(1, q, 8, 4, 4).astype(np.float32)
+    want = oracle.deform_attn(value, loc, attn, DINO_LEVELS)
+    got = run(hip, [value, loc, attn], DINO_LEVELS, "f32")
+    assert np.abs(got - want).max() <= 1e-4
+
+
+def test_pixel_centres_are_exact_gathers(hip):
+    """Locations at pixel centres with one-hot weights return the value rows bit for bit (power-of-two
+    level sizes, so (x + 0.5) / W * W - 0.5 is exact in f32)."""
+    shapes = [(8, 8), (4, 4)]
+    r = np.random.default_rng(3)
+    value = r.standard_normal((1, 80, 2, 16)).astype(np.float32)
+    xs, ys = r.integers(0, 4, (1, 5, 2, 2, 2)), r.integers(0, 4, (1, 5, 2, 2, 2))
+    loc = np.stack([(xs + 0.5) / np.array([8, 4]).reshape(1, 1, 1, 2, 1),
+                    (ys + 0.5) / np.array([8, 4]).reshape(1, 1, 1, 2, 1)], -1).astype(np.float32)
+    attn = np.zeros((1, 5, 2, 2, 2), np.float32)
+    attn[..., 1, 1] = 1.0
+    got = run(hip, [value, loc, attn], shapes, "f32").reshape(1, 5, 2, 16)
+    for qi in range(5):
+        for hi in range(2):
+            s_idx = 64 + ys[0, qi, hi, 1, 1] * 4 + xs[0, qi, hi, 1, 1]
+            assert np.array_equal(got[0, qi, hi], value[0, s_idx, hi])
+
+
+def test_deform_errors(hip):
+    v = torch.zeros(1, 30, 2, 8, device="cuda")
+    loc = torch.zeros(1, 3, 2, 5, 2, 2, device="cuda")
+    a = torch.zeros(1, 3, 2, 5, 2, device="cuda")
+    with pytest.raises(hip.SamHipError, match="at most 4 levels, got 5"):
+        hip.deform_attn(v, loc, a, [(2, 3)] * 5)
+    loc = torch.zeros(1, 3, 2, 2, 2, 2, device="cuda")
+    a = torch.zeros(1, 3, 2, 2, 2, device="cuda")
+    with pytest.raises(hip.SamHipError, match="pixels"):
+        hip.deform_attn(v, loc, a, [(2, 3), (2, 3)])

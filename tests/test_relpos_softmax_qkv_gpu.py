@@ -1,0 +1,78 @@
+"""Parity of relpos_softmax and qkv_split (libsam_hip.so) with the CPU oracle, on an MI355X.
+
+relpos_softmax follows the reference's own test (tests/kernels.rs:19-37): geometries (14,14,6,64),
+(64,64,2,64), (7,11,3,80), N(0,1) scores, q and table, scale 0.125, inputs rounded to the kernel dtype
+and the oracle run on the rounded values; max-abs 1e-3 on the probabilities (f16, the reference's bar),
+1e-5 relative for f32, and for bf16 1e-3 beyond the half-ulp rounding of the bf16 output itself.
+qkv_split is a permutation plus one rounded addition: bit-exact against the oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import sam_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+TORCH_DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import sam_hip
+
+    sam_hip.load()
+    assert torch.cuda.is_available(), "no GPU visible"
+    return sam_hip
+
+
+def dev(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", TORCH_DT[dtype])
+
+
+def half_ulp_bf16(x):
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -126)))
+    return 2.0 ** (e - 8)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("h,w,bh,hd", [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (2, 3, 2, 8), (16, 33, 1, 32)])
+def test_relpos_softmax_matches_oracle(hip, h, w, bh, hd, dtype):
+    print(f"relpos_softmax {dtype} {h}x{w} bh={bh} hd={hd}", flush=True)
+    n = h * w
+    r = np.random.default_rng(h * 100 + w)
+    s = oracle.round_to(r.standard_normal((bh, n, n)), dtype)
+    q = oracle.round_to(r.standard_normal((bh, n, hd)), dtype)
+    t = oracle.round_to(r.standard_normal((2 * h - 1 + 2 * w - 1, hd)), dtype)
+    want = oracle.relpos_softmax(s, q, t, h, w, 0.125)
+    got = hip.relpos_softmax(dev(s, dtype), dev(q, dtype), dev(t, dtype), h, w, 0.125)
+    got = got.float().cpu().numpy()
+    if dtype == "f32":
+        assert np.abs(got - want).max() / np.abs(want).max() <= 1e-5
+    elif dtype == "bf16":
+        assert (np.abs(got - want) - half_ulp_bf16(want)).max() <= 1e-3
+    else:
+        assert np.abs(got - want).max() <= 1e-3
+    np.testing.assert_allclose(got.sum(-1), 1.0, atol=2e-2 if dtype == "bf16" else 2e-3)
+
+
+def test_relpos_softmax_rejects_long_rows(hip):
+    s = torch.zeros(1, 91 * 91, 1, device="cuda", dtype=torch.float16)  # h*w = 8281 > 8192
+    q = torch.zeros(1, 91 * 91, 8, device="cuda", dtype=torch.float16)
+    t = torch.zeros(2 * 91 - 1 + 2 * 91 - 1, 8, device="cuda", dtype=torch.float16)
+    with pytest.raises(hip.SamHipError):
+        hip.relpos_softmax(s.expand(1, 91 * 91, 91 * 91), q, t, 91, 91, 0.1)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("n,nh,hd,win", [(196, 12, 64, 3), (196, 16, 80, 25), (4096, 16, 80, 1), (77, 3, 8, 2),
+                                         (5, 2, 6, 3)])
+def test_qkv_split_is_bit_exact(hip, n, nh, hd, win, dtype):
+    print(f"qkv_split {dtype} n={n} nh={nh} hd={hd} win={win}", flush=True)
+    r = np.random.default_rng(n + hd)
+    y = oracle.round_to(r.standard_normal((win * n, 3 * nh * hd)), dtype)
+    b = oracle.round_to(r.standard_normal(3 * nh * hd), dtype)
+    q0, k0, v0 = (oracle.round_to(x, dtype) for x in oracle.qkv_split(y, b, n, nh, hd))
+    q1, k1, v1 = hip.qkv_split(dev(y, dtype), dev(b, dtype), n, nh, hd)
+    for a, want in ((q1, q0), (k1, k0), (v1, v0)):
+        assert tuple(a.shape) == want.shape
+        assert np.array_equal(a.float().cpu().numpy(), want)
