@@ -68,7 +68,7 @@ def cpu_baseline():
 
     import sam_oracle
 
-    cores = os.cpu_count() or 1
+    cores = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
     r = np.random.default_rng(1)
 
     def time_layer(bh, h, w):

@@ -75,6 +75,45 @@ int sam_hip_qkv_split(const void* y, const void* bias, void* out, int dtype, lon
 int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, void* out, int dtype, int b, int s,
                         int q, int h, int d, int l, int p, const int* shapes, void* stream);
 
+/*
+ * Flash attention without a mask, f16 / bf16, on [b, l, h, d] operands given by (batch, row, head)
+ * element strides (NULL = contiguous [b, l, h, d]; the head dimension is always contiguous):
+ *   out[b, i, h, :] = softmax_j(scale * q[b,i,h,:] . k[b,j,h,:]) . v[b, :, h, :]
+ * Replaces the reference's GPU flash attention candle_flash_attn::flash_attn(q, k, v, scale, false)
+ * (sam2/hiera.rs:143-151, sam3/nn.rs:65-71, sam3/vision.rs:116-121), kernels::flash_attn_cpu
+ * (kernels.rs:910-915, cpu_gemm.rs:361-417) and sam3::nn::sdpa with mask None (sam3/nn.rs:26-34; pass
+ * [b, h, l, d] tensors as strides (h*l*d, d, l*d)). Lq != Lk is allowed.
+ * Optional RoPE, as SAM 2 memory attention applies it before sdpa (RopeAttn::forward,
+ * sam3/video.rs:106-141): the first n_rope_q queries and the first n_rope_k keys are rotated with the
+ * f32 tables rope_cos / rope_sin [rope_rows, d] (table row = index % rope_rows), the other rows are
+ * used as they are; n_rope_q = n_rope_k = 0 disables it (the tables may then be NULL).
+ * Workspace: sam_hip_flash_attn_workspace_size() bytes of device memory (16-byte aligned), for the
+ * key-split partial results and the rotated keys; it may be NULL when that size is 0. The size
+ * depends on the current device's CU count: query it on the device that runs the call.
+ * Limits: d % 8 == 0, d <= 256; scale >= 0; pointers and strides 16-byte aligned; out must not
+ * overlap k, v or the workspace. f32 is rejected (SAM_HIP_EDTYPE), as by the reference's GPU flash
+ * attention.
+ */
+long sam_hip_flash_attn_workspace_size(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k);
+int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, int dtype, int b, int lq, int lk,
+                       int h, int d, const long* strides_q, const long* strides_k, const long* strides_v,
+                       const long* strides_o, float scale, const float* rope_cos, const float* rope_sin,
+                       int rope_rows, int n_rope_q, int n_rope_k, void* workspace, long workspace_bytes,
+                       void* stream);
+
+/*
+ * 2-D axial RoPE on rows of a [b, l, h, d] tensor (strides as for flash attention, NULL = contiguous):
+ *   out[.., r, .., 2i]   = x[2i] * cos[t, 2i] - x[2i+1] * sin[t, 2i]
+ *   out[.., r, .., 2i+1] = x[2i+1] * cos[t, 2i+1] + x[2i] * sin[t, 2i+1]   (r < n_rot, t = r % rope_rows)
+ * in f32, each product and the sum rounded, then converted to dtype; rows r >= n_rot are copied.
+ * Replaces the reference's rope (sam3/video.rs:106-113) and its key tiling / pointer exclusion
+ * (sam3/video.rs:133-141); the tables are those of rope_tables_hd (sam3/vision.rs:26-46), f32.
+ * Limits: d % 8 == 0 (f16/bf16) or d % 4 == 0 (f32); pointers and strides 16-byte aligned.
+ */
+int sam_hip_rope(const void* x, const float* rope_cos, const float* rope_sin, void* out, int dtype, int b, int l,
+                 int h, int d, const long* strides_x, const long* strides_out, int rope_rows, int n_rot,
+                 void* stream);
+
 /* Message describing the last error returned on this thread ("" if none). */
 const char* sam_hip_last_error(void);
 

@@ -24,6 +24,8 @@ SOURCES = [
     "deform_attn.hip",
     "relpos_softmax.hip",
     "qkv_split.hip",
+    "flash_attn.hip",
+    "rope.hip",
     "sam_hip_abi.cpp",
 ]
 

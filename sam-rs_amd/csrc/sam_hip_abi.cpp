@@ -3,10 +3,12 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <string>
 
 #include "../../include/sam_hip.h"
+#include "flash_attn.hpp"
 
 namespace samhip {
 hipError_t attn_relpos_half(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out,
@@ -52,7 +54,7 @@ bool dtype_ok(int dtype) { return dtype == 0 || dtype == 1 || dtype == 2; }
 
 extern "C" {
 
-int sam_hip_abi_version(void) { return 1; }
+int sam_hip_abi_version(void) { return 2; }
 
 const char* sam_hip_last_error(void) { return g_last_error.c_str(); }
 
@@ -129,6 +131,167 @@ int sam_hip_qkv_split(const void* y, const void* bias, void* out, int dtype, lon
   if (blocks > 0x7fffffffL) return fail(SAM_HIP_EUNSUPPORTED, "qkv-split: too many tokens");
   hipError_t e = samhip::qkv_split(dtype, y, bias, out, tokens, n, nh, hd, reinterpret_cast<hipStream_t>(stream));
   return check_launch(e, "qkv-split");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------ flash attention
+
+namespace {
+
+void contiguous_strides(long* s, int l, int h, int d) {
+  s[0] = (long)l * h * d;
+  s[1] = (long)h * d;
+  s[2] = d;
+}
+
+// Strides of a [b, l, h, d] operand: the caller's, or those of the contiguous layout when null.
+int get_strides(const long* in, long* out, int l, int h, int d, int elem, const char* what) {
+  if (in) {
+    for (int i = 0; i < 3; ++i) out[i] = in[i];
+  } else {
+    contiguous_strides(out, l, h, d);
+  }
+  for (int i = 0; i < 3; ++i)
+    if (out[i] < 0 || (out[i] * elem) % 16 != 0)
+      return fail(SAM_HIP_EUNSUPPORTED, "flash-attn: %s strides must be non-negative multiples of 16 bytes", what);
+  return SAM_HIP_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int device_cus() {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+  }
+  return cus;
+}
+
+struct FlashPlan {
+  int qblocks, nsplit, tps;
+  size_t partial_bytes, rope_bytes, total;
+};
+
+FlashPlan plan_flash(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k) {
+  FlashPlan pl;
+  samhip::flash_plan(b, h, lq, lk, d, device_cus(), &pl.qblocks, &pl.nsplit, &pl.tps);
+  pl.partial_bytes = (samhip::flash_partial_bytes(b, h, lq, d, pl.nsplit) + 255) / 256 * 256;
+  const size_t elem = dtype == 0 ? 4 : 2;
+  pl.rope_bytes = n_rope_k > 0 ? (size_t)b * lk * h * d * elem : 0;
+  pl.total = pl.partial_bytes + pl.rope_bytes;
+  return pl;
+}
+
+int check_flash_sizes(int dtype, int b, int lq, int lk, int h, int d) {
+  if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
+  if (dtype == 0)
+    return fail(SAM_HIP_EDTYPE, "flash-attn: the MFMA flash kernel takes f16 or bf16 (the reference's GPU flash "
+                                "attention has the same limit); f32 attention goes through the CPU path");
+  if (b <= 0 || lq <= 0 || lk <= 0 || h <= 0 || d <= 0)
+    return fail(SAM_HIP_EINVAL, "flash-attn: sizes must be positive (b=%d lq=%d lk=%d h=%d d=%d)", b, lq, lk, h, d);
+  if (d % 8 != 0 || d > 256)
+    return fail(SAM_HIP_EUNSUPPORTED, "flash-attn: head dim must be a multiple of 8 and at most 256, got %d", d);
+  if ((long)b * h * lq >= (1L << 31) || (long)lk * 64 >= (1L << 31))
+    return fail(SAM_HIP_EUNSUPPORTED, "flash-attn: too many rows");
+  return SAM_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+long sam_hip_flash_attn_workspace_size(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k) {
+  if (check_flash_sizes(dtype, b, lq, lk, h, d) != SAM_HIP_OK) return -1;
+  return (long)plan_flash(dtype, b, lq, lk, h, d, n_rope_k).total;
+}
+
+int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, int dtype, int b, int lq, int lk, int h,
+                       int d, const long* strides_q, const long* strides_k, const long* strides_v,
+                       const long* strides_o, float scale, const float* rope_cos, const float* rope_sin,
+                       int rope_rows, int n_rope_q, int n_rope_k, void* workspace, long workspace_bytes,
+                       void* stream) {
+  if (!q || !k || !v || !out) return fail(SAM_HIP_EINVAL, "flash-attn: null pointer argument");
+  int rc = check_flash_sizes(dtype, b, lq, lk, h, d);
+  if (rc != SAM_HIP_OK) return rc;
+  if (!(scale >= 0.f) || scale > 3.0e38f)
+    return fail(SAM_HIP_EINVAL, "flash-attn: scale must be finite and non-negative, got %g", (double)scale);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(SAM_HIP_EUNSUPPORTED, "flash-attn: q, k, v and out must be 16-byte aligned");
+  if (n_rope_q < 0 || n_rope_k < 0 || n_rope_q > lq || n_rope_k > lk)
+    return fail(SAM_HIP_EINVAL, "flash-attn: rotated rows out of range (n_rope_q=%d of %d, n_rope_k=%d of %d)",
+                n_rope_q, lq, n_rope_k, lk);
+  if ((n_rope_q > 0 || n_rope_k > 0) && (!rope_cos || !rope_sin || rope_rows <= 0 || !aligned16(rope_cos) ||
+                                         !aligned16(rope_sin)))
+    return fail(SAM_HIP_EINVAL, "flash-attn: RoPE needs 16-byte aligned cos/sin tables with rope_rows > 0");
+  const int elem = dtype == 0 ? 4 : 2;
+  samhip::FlashParams p{};
+  if ((rc = get_strides(strides_q, p.sq, lq, h, d, elem, "q")) != SAM_HIP_OK) return rc;
+  if ((rc = get_strides(strides_k, p.sk, lk, h, d, elem, "k")) != SAM_HIP_OK) return rc;
+  if ((rc = get_strides(strides_v, p.sv, lk, h, d, elem, "v")) != SAM_HIP_OK) return rc;
+  if ((rc = get_strides(strides_o, p.so, lq, h, d, elem, "out")) != SAM_HIP_OK) return rc;
+  const FlashPlan pl = plan_flash(dtype, b, lq, lk, h, d, n_rope_k);
+  if (pl.total > 0 && (!workspace || workspace_bytes < (long)pl.total))
+    return fail(SAM_HIP_EINVAL, "flash-attn: needs a workspace of %zu bytes (sam_hip_flash_attn_workspace_size), got %ld",
+                pl.total, workspace ? workspace_bytes : 0L);
+  if (workspace && !aligned16(workspace)) return fail(SAM_HIP_EINVAL, "flash-attn: workspace must be 16-byte aligned");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.out = out;
+  if (n_rope_k > 0) {
+    // keys rotated into the workspace as a contiguous [b, lk, h, d] copy
+    void* kr = ws + pl.partial_bytes;
+    long sr[3];
+    contiguous_strides(sr, lk, h, d);
+    hipError_t e = samhip::rope_rows(dtype, k, p.sk, kr, sr, b, lk, h, d, rope_cos, rope_sin, rope_rows, n_rope_k, s);
+    if (e != hipSuccess) return check_launch(e, "flash-attn (key rotation)");
+    p.k = kr;
+    for (int i = 0; i < 3; ++i) p.sk[i] = sr[i];
+  }
+  p.b = b;
+  p.h = h;
+  p.lq = lq;
+  p.lk = lk;
+  p.d = d;
+  p.sc = scale * 1.4426950408889634f;
+  p.qblocks = pl.qblocks;
+  p.nsplit = pl.nsplit;
+  p.tps = pl.tps;
+  if (pl.nsplit > 1) {
+    p.opart = reinterpret_cast<float*>(ws);
+    p.ml = reinterpret_cast<float*>(ws + (size_t)pl.nsplit * b * h * lq * samhip::flash_padded_dim(d) * sizeof(float));
+  }
+  p.rcos = rope_cos;
+  p.rsin = rope_sin;
+  p.rrows = rope_rows;
+  p.nrq = n_rope_q;
+  return check_launch(samhip::flash_attn_half(dtype, p, n_rope_q > 0, s), "flash-attn");
+}
+
+int sam_hip_rope(const void* x, const float* cos_t, const float* sin_t, void* out, int dtype, int b, int l, int h,
+                 int d, const long* strides_x, const long* strides_out, int rope_rows, int n_rot, void* stream) {
+  if (!x || !cos_t || !sin_t || !out) return fail(SAM_HIP_EINVAL, "rope: null pointer argument");
+  if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
+  if (b <= 0 || l <= 0 || h <= 0 || d <= 0 || rope_rows <= 0)
+    return fail(SAM_HIP_EINVAL, "rope: sizes must be positive (b=%d l=%d h=%d d=%d rope_rows=%d)", b, l, h, d,
+                rope_rows);
+  const int per = dtype == 0 ? 4 : 8;
+  if (d % per != 0) return fail(SAM_HIP_EUNSUPPORTED, "rope: head dim must be a multiple of %d, got %d", per, d);
+  if (n_rot < 0 || n_rot > l) return fail(SAM_HIP_EINVAL, "rope: n_rot=%d outside [0, %d]", n_rot, l);
+  if (!aligned16(x) || !aligned16(out)) return fail(SAM_HIP_EUNSUPPORTED, "rope: x and out must be 16-byte aligned");
+  const int elem = dtype == 0 ? 4 : 2;
+  long sx[3], so[3];
+  int rc;
+  if ((rc = get_strides(strides_x, sx, l, h, d, elem, "x")) != SAM_HIP_OK) return rc;
+  if ((rc = get_strides(strides_out, so, l, h, d, elem, "out")) != SAM_HIP_OK) return rc;
+  if ((long)b * l * h * (d / per) >= (1L << 40)) return fail(SAM_HIP_EUNSUPPORTED, "rope: too many elements");
+  return check_launch(samhip::rope_rows(dtype, x, sx, out, so, b, l, h, d, cos_t, sin_t, rope_rows, n_rot,
+                                        reinterpret_cast<hipStream_t>(stream)),
+                      "rope");
 }
 
 }  // extern "C"

@@ -10,6 +10,8 @@ Names, argument meaning and errors follow the reference:
     deform_attn(value, loc, attn, shapes)                kernels.rs:824-835
     flash_attn(q, k, v, scale=None)                      kernels.rs:910-915 / candle_flash_attn::flash_attn
     sdpa(q, k, v, mask=None)                             sam3/nn.rs:26-34
+    rope(x, cos, sin)                                    sam3/video.rs:106-113
+    rope_attention(q, k, v, cos, sin, n_exclude)         sam3/video.rs:129-145 (after the projections)
 
 There is no CPU fallback: on a machine without the built library or a GPU every call raises.
 """
@@ -51,6 +53,14 @@ def load():
         L.sam_hip_relpos_softmax.restype = _i
         L.sam_hip_qkv_split.argtypes = [_vp] * 3 + [_i, ctypes.c_long, _i, _i, _i, _vp]
         L.sam_hip_qkv_split.restype = _i
+        _lp = ctypes.POINTER(ctypes.c_long)
+        L.sam_hip_flash_attn_workspace_size.argtypes = [_i] * 7
+        L.sam_hip_flash_attn_workspace_size.restype = ctypes.c_long
+        L.sam_hip_flash_attn.argtypes = [_vp] * 4 + [_i] * 6 + [_lp] * 4 + [_f, _vp, _vp, _i, _i, _i, _vp,
+                                                                        ctypes.c_long, _vp]
+        L.sam_hip_flash_attn.restype = _i
+        L.sam_hip_rope.argtypes = [_vp] * 4 + [_i] * 5 + [_lp] * 2 + [_i, _i, _vp]
+        L.sam_hip_rope.restype = _i
         _lib = L
     return _lib
 
@@ -159,3 +169,115 @@ def qkv_split(y: torch.Tensor, bias: torch.Tensor, n: int, nh: int, hd: int):
     packed = torch.empty((3, t * nh * hd), dtype=y.dtype, device=y.device)
     _check(load().sam_hip_qkv_split(y.data_ptr(), bias.data_ptr(), packed.data_ptr(), dt, t, n, nh, hd, _stream()))
     return packed[0].view(bh, n, hd), packed[1].view(bh, hd, n), packed[2].view(bh, n, hd)
+
+
+def _strides_blhd(t: torch.Tensor, layout: str):
+    """(batch, row, head) element strides of a 4-d tensor in the [B, L, H, D] or [B, H, L, D] layout;
+    the head dimension must be contiguous."""
+    if t.stride(3) != 1:
+        raise SamHipError("sam-rs kernels need contiguous inputs")  # kernels.rs:1100
+    if layout == "blhd":
+        s = (t.stride(0), t.stride(1), t.stride(2))
+    else:
+        s = (t.stride(0), t.stride(2), t.stride(1))
+    return (ctypes.c_long * 3)(*s)
+
+
+def _flash(q, k, v, out, layout: str, scale: float, cos=None, sin=None, n_rope_q: int = 0, n_rope_k: int = 0):
+    for t in (q, k, v):
+        if not t.is_cuda:
+            raise SamHipError("sam-rs HIP kernels need device tensors")
+    dt = _dtype(q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
+        raise SamHipError(f"flash-attn: incompatible q/k/v shapes {tuple(q.shape)}/{tuple(k.shape)}/{tuple(v.shape)}")
+    if layout == "blhd":
+        b, lq, h, d = q.shape
+        kb, lk, kh, kd = k.shape
+    else:
+        b, h, lq, d = q.shape
+        kb, kh, lk, kd = k.shape
+    if (kb, kh, kd) != (b, h, d):  # kernels.rs:425-427
+        raise SamHipError(f"flash-attn: incompatible q/k/v shapes {tuple(q.shape)}/{tuple(k.shape)}/{tuple(v.shape)}")
+    L = load()
+    ws_bytes = L.sam_hip_flash_attn_workspace_size(dt, b, lq, lk, h, d, n_rope_k)
+    if ws_bytes < 0:
+        raise SamHipError(L.sam_hip_last_error().decode())
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    rc = L.sam_hip_flash_attn(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dt, b, lq, lk, h, d,
+                              _strides_blhd(q, layout), _strides_blhd(k, layout), _strides_blhd(v, layout),
+                              _strides_blhd(out, layout), scale,
+                              cos.data_ptr() if cos is not None else None, sin.data_ptr() if sin is not None else None,
+                              cos.shape[0] if cos is not None else 0, n_rope_q, n_rope_k, ws.data_ptr(), ws_bytes,
+                              _stream())
+    _check(rc)
+    return out
+
+
+def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None) -> torch.Tensor:
+    """softmax(scale * q k^T) v without a mask on q [B, Lq, H, D], k/v [B, Lk, H, D] -> [B, Lq, H, D]
+    (f16 / bf16), as candle_flash_attn::flash_attn(q, k, v, scale, false) and kernels::flash_attn_cpu
+    compute it. scale defaults to D^-0.5, the value every reference caller passes."""
+    d = q.shape[-1]
+    scale = float(d) ** -0.5 if scale is None else float(scale)
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    return _flash(q, k, v, out, "blhd", scale)
+
+
+def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask=None) -> torch.Tensor:
+    """sam3::nn::sdpa on [B, H, L, D] tensors: softmax(q k^T * D^-0.5) v. Only mask=None, the form
+    SAM 2 memory attention uses, runs on the GPU kernel; a mask raises."""
+    if mask is not None:
+        raise SamHipError("sdpa: the HIP flash kernel takes no additive mask")
+    d = q.shape[-1]
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    return _flash(q, k, v, out, "bhld", float(d) ** -0.5)
+
+
+def _rope_tables(cos: torch.Tensor, sin: torch.Tensor, d: int, device):
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != d:
+        raise SamHipError(f"rope: tables must be [rows, {d}], got {tuple(cos.shape)} and {tuple(sin.shape)}")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise SamHipError("rope: the cos/sin tables are f32 (sam3/vision.rs:26-46)")
+    if cos.device != device or sin.device != device:
+        raise SamHipError("rope: the tables must be on the same device as x")
+    return cos.contiguous(), sin.contiguous()
+
+
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_rot: int | None = None) -> torch.Tensor:
+    """x * cos + rotate_pairwise(x) * sin in f32 over x [B, L, D] (or [B, L, H, D]), tables [T, D];
+    row r uses table row r % T. Rows r >= n_rot (default: all rotated) are copied unchanged."""
+    squeeze = x.dim() == 3
+    x4 = x.unsqueeze(2) if squeeze else x
+    if x4.dim() != 4:
+        raise SamHipError(f"rope: x must be [B, L, D] or [B, L, H, D], got {tuple(x.shape)}")
+    b, l, h, d = x4.shape
+    cos, sin = _rope_tables(cos, sin, d, x.device)
+    n_rot = l if n_rot is None else int(n_rot)
+    dt = _dtype(x4)
+    out = torch.empty((b, l, h, d), dtype=x.dtype, device=x.device)
+    _check(load().sam_hip_rope(x4.data_ptr(), cos.data_ptr(), sin.data_ptr(), out.data_ptr(), dt, b, l, h, d,
+                               _strides_blhd(x4, "blhd"), None, cos.shape[0], n_rot, _stream()))
+    return out.squeeze(2) if squeeze else out
+
+
+def rope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                   n_exclude: int) -> torch.Tensor:
+    """The attention core of RopeAttn::forward (sam3/video.rs:129-145) after the projections, one head:
+    q [B, Lq, D] rotated with the tables, the first M - n_exclude keys of k [B, M, D] rotated with the
+    tables tiled to their length, the last n_exclude (object pointers) not, then sdpa with v [B, M, D].
+    Returns [B, Lq, D]."""
+    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape:
+        raise SamHipError(f"rope_attention: q [B, Lq, D] and k, v [B, M, D], got {tuple(q.shape)}, "
+                          f"{tuple(k.shape)}, {tuple(v.shape)}")
+    b, lq, d = q.shape
+    m = k.shape[1]
+    cos, sin = _rope_tables(cos, sin, d, q.device)
+    rot = m - n_exclude
+    if n_exclude < 0 or rot < 0 or rot % cos.shape[0] != 0:
+        raise SamHipError(f"rope_attention: {rot} rotated keys is not a whole number of {cos.shape[0]}-row tables")
+    if lq > cos.shape[0]:
+        raise SamHipError(f"rope_attention: {lq} queries but the tables have {cos.shape[0]} rows")
+    out = torch.empty((b, lq, d), dtype=q.dtype, device=q.device)
+    _flash(q.unsqueeze(2), k.unsqueeze(2), v.unsqueeze(2), out.unsqueeze(2), "blhd", float(d) ** -0.5, cos, sin,
+           lq, rot)
+    return out

@@ -1,0 +1,39 @@
+"""Parity bars shared by the GPU tests (the bars the reference's numerics call for).
+
+f32: max|gpu - cpu| / max|cpu| <= 1e-5. f16 / bf16: max-abs <= 2e-3 on attention outputs against the
+f32 oracle run on inputs pre-rounded to the kernel dtype (as tests/kernels.rs:28-31 does); bf16 is
+measured beyond the half-ulp rounding of the bf16 output itself.
+"""
+import numpy as np
+import torch
+
+F32_REL_TOL = 1e-5
+HALF_ABS_TOL = 2e-3
+TORCH_DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def to_dev(x, dtype):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(device="cuda", dtype=TORCH_DT[dtype])
+
+
+def bf16_half_ulp(x):
+    """Half the spacing of bf16 numbers at |x| (8 significant bits): the rounding any bf16 output has."""
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -126)))
+    return 2.0 ** (e - 8)
+
+
+def check(got, want, dtype, what):
+    """f32: max|gpu-cpu| / max|cpu| <= 1e-5. f16: max-abs <= 2e-3. bf16: max-abs <= 2e-3 beyond the
+    half-ulp rounding of the bf16 output itself (|out| >= 0.5 has a half-ulp of 2e-3 or more, so no
+    bf16 result can meet a bare 2e-3 there)."""
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    if dtype == "f32":
+        err = np.abs(got - want).max() / np.abs(want).max()
+        assert err <= F32_REL_TOL, f"{what}: max|gpu-cpu|/max|cpu| = {err:.3g}"
+    elif dtype == "bf16":
+        err = (np.abs(got - want) - bf16_half_ulp(want)).max()
+        assert err <= HALF_ABS_TOL, f"{what}: max abs diff beyond bf16 output rounding {err:.3g}"
+    else:
+        err = np.abs(got - want).max()
+        assert err <= HALF_ABS_TOL, f"{what}: max abs diff {err:.3g}"
+    return err

@@ -27,7 +27,8 @@ def lib():
 def test_header_declares_the_entry_points():
     names = declared_functions()
     for want in ("sam_hip_attn_relpos", "sam_hip_relpos_softmax", "sam_hip_qkv_split", "sam_hip_deform_attn",
-                 "sam_hip_last_error", "sam_hip_abi_version"):
+                 "sam_hip_flash_attn", "sam_hip_flash_attn_workspace_size", "sam_hip_rope", "sam_hip_last_error",
+                 "sam_hip_abi_version"):
         assert want in names
 
 
@@ -54,6 +55,31 @@ def test_null_pointers_and_bad_sizes_fail_without_a_launch(lib):
     assert lib.sam_hip_deform_attn(fake, fake, fake, fake, 0, 1, 31, 3, 2, 8, 2, 2, shapes, None) == 1
     lib.sam_hip_qkv_split.argtypes = [vp] * 3 + [i, ctypes.c_long, i, i, i, vp]
     assert lib.sam_hip_qkv_split(fake, fake, fake, 1, 100, 7, 2, 8, None) == 1  # 100 % 7 != 0
+
+
+def test_flash_and_rope_argument_checks(lib):
+    lib.sam_hip_last_error.restype = ctypes.c_char_p
+    vp, i, f, lp = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.POINTER(ctypes.c_long)
+    lib.sam_hip_flash_attn.argtypes = [vp] * 4 + [i] * 6 + [lp] * 4 + [f, vp, vp, i, i, i, vp, ctypes.c_long, vp]
+    lib.sam_hip_flash_attn_workspace_size.argtypes = [i] * 7
+    lib.sam_hip_flash_attn_workspace_size.restype = ctypes.c_long
+    fake = vp(0x1000)
+    args = lambda dt, d, scale=0.1: (fake, fake, fake, fake, dt, 1, 8, 8, 1, d, None, None, None, None, scale, None,
+                                     None, 0, 0, 0, None, 0, None)
+    assert lib.sam_hip_flash_attn(None, None, None, None, 1, 1, 8, 8, 1, 64, None, None, None, None, 0.1, None,
+                                  None, 0, 0, 0, None, 0, None) == 1
+    assert lib.sam_hip_flash_attn(*args(0, 64)) == 2
+    assert b"f16 or bf16" in lib.sam_hip_last_error()
+    assert lib.sam_hip_flash_attn(*args(1, 20)) == 3
+    assert lib.sam_hip_flash_attn(*args(1, 264)) == 3
+    assert lib.sam_hip_flash_attn(*args(1, 64, -1.0)) == 1
+    assert lib.sam_hip_flash_attn_workspace_size(1, 1, 8, 8, 1, 20, 0) == -1
+    # RoPE asked for without tables
+    assert lib.sam_hip_flash_attn(fake, fake, fake, fake, 1, 1, 8, 8, 1, 64, None, None, None, None, 0.1, None, None,
+                                  0, 8, 0, None, 0, None) == 1
+    lib.sam_hip_rope.argtypes = [vp] * 4 + [i] * 5 + [lp] * 2 + [i, i, vp]
+    assert lib.sam_hip_rope(fake, fake, fake, fake, 1, 1, 8, 1, 12, None, None, 8, 8, None) == 3
+    assert lib.sam_hip_rope(fake, fake, fake, fake, 1, 1, 8, 1, 16, None, None, 8, 9, None) == 1
 
 
 def test_abi_version(lib):

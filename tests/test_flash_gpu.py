@@ -1,0 +1,186 @@
+"""Parity of the flash-attention, RoPE and memory-attention entry points (libsam_hip.so) with the CPU
+oracle, on an MI355X.
+
+The oracle restates the reference's attention back ends on the same seeded inputs, pre-rounded to the
+kernel dtype (as tests/kernels.rs:28-31 does): sdpa (sam3/nn.rs:26-34) for the [B, H, L, D] layout,
+the per-(batch, query, head) scalar attention for the [B, L, H, D] layout that flash_attn_cpu and
+candle_flash_attn take (kernels.rs:416-434), rope (sam3/video.rs:106-113) and RopeAttn's core
+(sam3/video.rs:129-145). Bars: f16/bf16 max-abs 2e-3 against the f32 oracle; RoPE bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import sam_oracle as oracle
+from parity import TORCH_DT, check, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import sam_hip
+
+    sam_hip.load()
+    assert torch.cuda.is_available(), "no GPU visible"
+    return sam_hip
+
+
+def rounded(r, shape, dtype, std=1.0):
+    return oracle.round_to((std * r.standard_normal(shape)).astype(np.float32), dtype)
+
+
+# (b, lq, lk, h, d): tiny and ragged shapes (partial key tiles, partial query blocks, one key), the
+# head dims of the reference's callers (Hiera 96 at its widest stage, SAM 3 ViT 64, memory attention
+# 256), and shapes whose few query blocks force the key-split path.
+BLHD = [(1, 5, 7, 2, 16), (2, 33, 65, 3, 64), (1, 40, 100, 1, 256), (2, 130, 200, 4, 96), (1, 64, 64, 8, 64),
+        (1, 300, 1000, 2, 128), (1, 1, 1, 1, 8), (1, 17, 3000, 1, 64), (3, 49, 49, 2, 32), (1, 257, 129, 1, 256)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("b,lq,lk,h,d", BLHD)
+def test_flash_attn_matches_oracle(hip, b, lq, lk, h, d, dtype):
+    r = np.random.default_rng(1000 + lq + lk + d)
+    q, k, v = (rounded(r, (b, n, h, d), dtype) for n in (lq, lk, lk))
+    got = hip.flash_attn(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype))
+    torch.cuda.synchronize()
+    want = oracle.mha_blhd(q, k, v)
+    check(got.float().cpu().numpy(), want, dtype, f"flash_attn b{b} lq{lq} lk{lk} h{h} d{d} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("b,h,lq,lk,d", [(1, 1, 5, 7, 16), (2, 3, 33, 65, 64), (1, 1, 40, 100, 256),
+                                         (1, 2, 200, 700, 256)])
+def test_sdpa_bhld_layout(hip, b, h, lq, lk, d, dtype):
+    r = np.random.default_rng(7 + lq)
+    q, k, v = (rounded(r, (b, h, n, d), dtype) for n in (lq, lk, lk))
+    got = hip.sdpa(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype))
+    torch.cuda.synchronize()
+    check(got.float().cpu().numpy(), oracle.sdpa(q, k, v), dtype, f"sdpa {b}x{h}x{lq}x{lk}x{d} {dtype}")
+
+
+def test_strided_views_are_read_in_place(hip):
+    """A [B, L, H, D] slice of a wider packed projection (row stride > H*D) gives the same result as
+    its contiguous copy."""
+    r = np.random.default_rng(3)
+    b, l, h, d = 2, 90, 2, 64
+    packed = to_dev(rounded(r, (b, l, 3, h, d), "f16"), "f16")
+    q, k, v = packed[:, :, 0], packed[:, :, 1], packed[:, :, 2]
+    got = hip.flash_attn(q, k, v)
+    ref = hip.flash_attn(q.contiguous(), k.contiguous(), v.contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_rope_is_bit_exact(hip, dtype):
+    """rope rounds like the reference: f32 products and sum, then one rounding to the dtype."""
+    side, d = 8, 256
+    cos, sin = oracle.rope_tables(side, 1.0, d, 10000.0)
+    r = np.random.default_rng(5)
+    x = rounded(r, (3 * side * side, d), dtype)
+    got = hip.rope(to_dev(x, dtype).unsqueeze(0), torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda())
+    torch.cuda.synchronize()
+    want = oracle.round_to(np.concatenate([oracle.rope(x[i * 64:(i + 1) * 64], cos, sin) for i in range(3)]), dtype)
+    assert np.array_equal(got[0].float().cpu().numpy(), want)
+
+
+def test_rope_leaves_excluded_rows(hip):
+    side, d = 4, 64
+    cos, sin = oracle.rope_tables(side, 1.0, d, 10000.0)
+    r = np.random.default_rng(6)
+    x = rounded(r, (2 * 16 + 5, d), "f16")
+    got = hip.rope(to_dev(x, "f16").unsqueeze(0), torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda(),
+                   n_rot=32)[0].float().cpu().numpy()
+    assert np.array_equal(got[32:], x[32:])
+    want = oracle.round_to(np.concatenate([oracle.rope(x[:16], cos, sin), oracle.rope(x[16:32], cos, sin)]), "f16")
+    assert np.array_equal(got[:32], want)
+
+
+def memory_inputs(side, frames, n_ptr, d, dtype, seed):
+    r = np.random.default_rng(seed)
+    n = side * side
+    m = frames * n + n_ptr
+    q = rounded(r, (n, d), dtype)
+    k = rounded(r, (m, d), dtype)
+    v = rounded(r, (m, d), dtype)
+    cos, sin = oracle.rope_tables(side, 1.0, d, 10000.0)
+    return q, k, v, cos, sin
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("side,frames,n_ptr", [(8, 1, 0), (8, 3, 8), (6, 2, 4)])
+def test_rope_attention_small(hip, side, frames, n_ptr, dtype):
+    """RopeAttn's attention core: self-attention (frames 1, no pointers) and cross-attention over tiled
+    memory frames plus unrotated object-pointer tokens."""
+    q, k, v, cos, sin = memory_inputs(side, frames, n_ptr, 256, dtype, 11 + side + frames)
+    got = hip.rope_attention(to_dev(q, dtype)[None], to_dev(k, dtype)[None], to_dev(v, dtype)[None],
+                             torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda(), n_ptr)
+    torch.cuda.synchronize()
+    # the reference rounds the rotated q and k to the dtype before sdpa (rope converts back, video.rs:112)
+    qr = oracle.round_to(oracle.rope(q, cos, sin), dtype)
+    rot = k.shape[0] - n_ptr
+    kr = np.concatenate([oracle.round_to(oracle.rope(k[i:i + len(cos)], cos, sin), dtype)
+                         for i in range(0, rot, len(cos))] + [k[rot:]])
+    want = oracle.sdpa(qr[None, None], kr[None, None], v[None, None])[0, 0]
+    check(got[0].float().cpu().numpy(), want, dtype, f"rope_attention side{side} frames{frames} ptr{n_ptr}")
+    # and, in f16, against the oracle's own f32 RopeAttn core (rotated q/k kept in f32): f16 rounding of
+    # the rotated q/k stays inside the bar; bf16's (2^-9 of each score) does not, as in the reference
+    if dtype == "f16":
+        want32 = oracle.rope_attention(q, k, v, cos, sin, n_ptr)
+        check(got[0].float().cpu().numpy(), want32, dtype, "rope_attention vs f32 rotation")
+
+
+@pytest.mark.parametrize("case", ["self", "cross"])
+def test_sam2_memory_attention_full_size(hip, case):
+    """SAM 2.1 memory attention at its real size (f16, d 256, 64x64 grid): self-attention over 4096
+    tokens, cross-attention over 7 memory frames x 4096 + 64 pointer tokens = 28736 keys. The oracle
+    checks 96 query rows spread over the grid (each output row depends only on its own query)."""
+    frames, n_ptr = (1, 0) if case == "self" else (7, 64)
+    q, k, v, cos, sin = memory_inputs(64, frames, n_ptr, 256, "f16", 21 if case == "self" else 22)
+    got = hip.rope_attention(to_dev(q, "f16")[None], to_dev(k, "f16")[None], to_dev(v, "f16")[None],
+                             torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda(), n_ptr)
+    torch.cuda.synchronize()
+    got = got[0].float().cpu().numpy()
+    assert np.isfinite(got).all()
+    rows = np.linspace(0, 4095, 96).astype(int)
+    qr = oracle.round_to(oracle.rope(q, cos, sin), "f16")[rows]
+    rot = k.shape[0] - n_ptr
+    kr = np.concatenate([oracle.round_to(oracle.rope(k[i:i + 4096], cos, sin), "f16") for i in range(0, rot, 4096)]
+                        + [k[rot:]])
+    want = oracle.sdpa(qr[None, None], kr[None, None], v[None, None])[0, 0]
+    check(got[rows], want, "f16", f"memory attention {case}")
+
+
+def test_full_size_properties(hip):
+    """Size-independent properties at the cross-attention size: identical keys give the mean of v
+    (uniform softmax), and permuting keys together with values leaves the output unchanged."""
+    g = torch.Generator(device="cuda").manual_seed(4)
+    lq, lk, d = 4096, 28736, 256
+    q = torch.randn(1, lq, 1, d, device="cuda", generator=g).half()
+    v = torch.randn(1, lk, 1, d, device="cuda", generator=g).half()
+    k1 = torch.randn(1, 1, 1, d, device="cuda", generator=g).half().expand(1, lk, 1, d).contiguous()
+    out = hip.flash_attn(q, k1, v)
+    mean = v.float().mean(dim=1, keepdim=True)
+    assert (out.float() - mean).abs().max().item() <= 2e-3
+    k = torch.randn(1, lk, 1, d, device="cuda", generator=g).half()
+    perm = torch.randperm(lk, device="cuda", generator=g)
+    o1 = hip.flash_attn(q, k, v)
+    o2 = hip.flash_attn(q, k[:, perm].contiguous(), v[:, perm].contiguous())
+    assert (o1.float() - o2.float()).abs().max().item() <= 2e-3
+
+
+def test_flash_errors(hip):
+    x16 = torch.zeros(1, 8, 1, 64, device="cuda", dtype=torch.float16)
+    with pytest.raises(hip.SamHipError, match="f16 or bf16"):
+        hip.flash_attn(x16.float(), x16.float(), x16.float())
+    with pytest.raises(hip.SamHipError, match="multiple of 8"):
+        y = torch.zeros(1, 8, 1, 20, device="cuda", dtype=torch.float16)
+        hip.flash_attn(y, y, y)
+    with pytest.raises(hip.SamHipError, match="incompatible"):
+        hip.flash_attn(x16, torch.zeros(1, 8, 2, 64, device="cuda", dtype=torch.float16), x16)
+    with pytest.raises(hip.SamHipError, match="mask"):
+        hip.sdpa(x16, x16, x16, mask=x16)
+    with pytest.raises(hip.SamHipError, match="dtype mismatch"):
+        hip.flash_attn(x16, x16.bfloat16(), x16)
+    assert TORCH_DT["f16"] == torch.float16
