@@ -6,13 +6,17 @@ One step = the attention core of every encoder layer of ViT-H for one batch of 1
 fused rel-pos attention kernel on inputs already resident in HBM (fresh q/kT/v per layer).
 
 Prints one JSON line: ms per image, the global-layer kernel's achieved TFLOP/s against the f16 MFMA
-peak (timed live with HIP events on the launch stream), and the CPU oracle timed on this host.
+peak (timed live with HIP events on the launch stream), and the CPU oracle timed on this host. A
+"secondary" object times the other kernels of the path at their workload shapes: SAM 2.1 memory
+attention (4 layers, f16), Grounding DINO-tiny deformable attention (f32) and the ViT-B f32 layers.
 
     python bench.py [--steps K] [--warmup W] [--batch B] [--dtype f16|bf16] [--no-cpu-baseline]
+                    [--no-secondary] [--layers all|global|window] [--copy-probe]
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -26,6 +30,7 @@ HBM_PEAK_GBS = 8000.0
 GLOBAL_LAYERS = (7, 15, 23, 31)
 DEPTH, HEADS, HD = 32, 16, 80
 WINDOWS = 25  # 64x64 tokens padded to 70x70 -> 5 x 5 windows of 14x14
+CODE = {"f32": 0, "f16": 1, "bf16": 2}
 
 
 def parse():
@@ -36,8 +41,11 @@ def parse():
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--dtype", default="f16", choices=["f16", "bf16"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--layers", default="all", choices=["all", "global", "window"],
                     help="restrict the step to one layer kind (for profiling one kernel)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a device copy of 256 MiB five times (the PMC byte-counter calibration)")
     return ap.parse_args()
 
 
@@ -52,17 +60,18 @@ def layer_shapes(batch):
     return out
 
 
-def flops(bh, n):
-    return 4.0 * bh * n * n * HD
+def flops(bh, n, hd=HD):
+    return 4.0 * bh * n * n * hd
 
 
-def window_bytes(bh, n, elem=2):
-    return float(bh) * n * HD * elem * 4  # q, kT, v read once, out written once
+def window_bytes(bh, n, elem=2, hd=HD):
+    return float(bh) * n * hd * elem * 4  # q, kT, v read once, out written once
 
 
 def cpu_baseline():
-    """The oracle (C restatement of the reference's exact-f32 CPU attention, OpenMP on every host core)
-    on one image's windowed layer and one image's global layer; ms/image = 28 x window + 4 x global."""
+    """The oracle (C restatement of the reference's exact-f32 CPU attention, OpenMP on the host
+    threads) on one image's windowed layer and one image's global layer; ms/image = 28 x window +
+    4 x global."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
@@ -71,23 +80,26 @@ def cpu_baseline():
     cores = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
     r = np.random.default_rng(1)
 
-    def time_layer(bh, h, w):
+    def time_layer(bh, h, w, reps):
         n = h * w
         q = r.standard_normal((bh, n, HD), dtype=np.float32)
         kt = r.standard_normal((bh, HD, n), dtype=np.float32)
         v = r.standard_normal((bh, n, HD), dtype=np.float32)
         table = (0.02 * r.standard_normal((2 * h - 1 + 2 * w - 1, HD))).astype(np.float32)
-        t0 = time.perf_counter()
-        sam_oracle.attention_relpos(q, kt, v, table, h, w, HD ** -0.5, nthreads=cores)
-        return time.perf_counter() - t0
+        best = float("inf")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            sam_oracle.attention_relpos(q, kt, v, table, h, w, HD ** -0.5, nthreads=cores)
+            best = min(best, time.perf_counter() - t0)
+        return best
 
-    t_win = time_layer(WINDOWS * HEADS, 14, 14)
-    t_glob = time_layer(HEADS, 64, 64)
+    t_win = time_layer(WINDOWS * HEADS, 14, 14, 5)
+    t_glob = time_layer(HEADS, 64, 64, 3)
     ms = 1e3 * ((DEPTH - len(GLOBAL_LAYERS)) * t_win + len(GLOBAL_LAYERS) * t_glob)
     return {
         "value": round(ms, 1), "unit": "ms/image", "cores": cores, "kind": "port",
         "sample": "one windowed layer (400 x 14x14) and one global layer (16 x 64x64) of one image, f32, "
-                  f"timed once each ({t_win:.2f} s, {t_glob:.2f} s) and scaled by 28 and 4 layers",
+                  f"best of 5 and 3 runs ({t_win:.3f} s, {t_glob:.3f} s) scaled by 28 and 4 layers",
     }
 
 
@@ -99,6 +111,154 @@ def traffic_from_profiles():
     return None
 
 
+class Timer:
+    """HIP events recorded on the launch stream around each call; the average launch time in ms."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+
+    def avg_ms(self, fn, reps, warmup=2):
+        for _ in range(warmup):
+            fn()
+        ev = [(self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True))
+              for _ in range(reps)]
+        for a, b in ev:
+            a.record(self.stream)
+            fn()
+            b.record(self.stream)
+        self.torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in ev) / reps
+
+
+def check(lib, rc):
+    if rc:
+        raise RuntimeError(lib.sam_hip_last_error().decode())
+
+
+def secondary(torch, sam_hip, lib, dev, sp, timer):
+    """The other kernels of the path at their workload shapes (synthetic inputs resident in HBM)."""
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(7)
+    vp = ctypes.c_void_p
+
+    # SAM 2.1 memory attention: per layer self-attention (4096 x 4096) and cross-attention
+    # (4096 x 7*4096 + 64 pointer tokens), one head, d 256, 2-D RoPE (theta 1e4) on a 64x64 grid.
+    sys.path.insert(0, os.path.join(ROOT, "sam-rs_amd"))
+    import math
+
+    side, d, lq, mk, nptr = 64, 256, 4096, 7 * 4096 + 64, 64
+    sp_ = d // 2
+    inv = torch.tensor([1.0 / 10000.0 ** (2.0 * i / sp_) for i in range(sp_ // 2)], dtype=torch.float32)
+    t = torch.arange(side * side)
+    pos = torch.stack([(t % side).float(), (t // side).float()], 1)  # (col, row)
+    ang = torch.cat([pos[:, :1] * inv, pos[:, 1:] * inv], 1)  # [N, sp]
+    cos = torch.cos(ang).repeat_interleave(2, 1).contiguous().to(dev)
+    sin = torch.sin(ang).repeat_interleave(2, 1).contiguous().to(dev)
+    layers = []
+    for _ in range(4):
+        q = torch.randn(1, lq, 1, d, device=dev, generator=g).half()
+        ks = torch.randn(1, lq, 1, d, device=dev, generator=g).half()
+        vs = torch.randn(1, lq, 1, d, device=dev, generator=g).half()
+        kc = torch.randn(1, mk, 1, d, device=dev, generator=g).half()
+        vc = torch.randn(1, mk, 1, d, device=dev, generator=g).half()
+        layers.append((q, ks, vs, kc, vc, torch.empty_like(q)))
+    ws_bytes = max(lib.sam_hip_flash_attn_workspace_size(1, 1, lq, mk, 1, d, mk - nptr),
+                   lib.sam_hip_flash_attn_workspace_size(1, 1, lq, lq, 1, d, lq))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    scale = d ** -0.5
+
+    def attn(q, k, v, out, lk, nrk):
+        check(lib, lib.sam_hip_flash_attn(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), 1, 1, lq, lk, 1,
+                                          d, None, None, None, None, scale, vp(cos.data_ptr()), vp(sin.data_ptr()),
+                                          side * side, lq, nrk, vp(ws.data_ptr()), ws_bytes, sp))
+
+    def mem_step():
+        for q, ks, vs, kc, vc, out in layers:
+            attn(q, ks, vs, out, lq, lq)
+            attn(q, kc, vc, out, mk, mk - nptr)
+
+    self_ms = timer.avg_ms(lambda: attn(*layers[0][:3], layers[0][5], lq, lq), 20)
+    cross_ms = timer.avg_ms(lambda: attn(layers[0][0], layers[0][3], layers[0][4], layers[0][5], mk, mk - nptr), 20)
+    total_ms = timer.avg_ms(mem_step, 5)
+    f_self, f_cross = 4.0 * lq * lq * d, 4.0 * lq * mk * d
+    res["sam2_memory_attention_f16"] = {
+        "workload": "SAM 2.1 memory attention, 4 layers x (self 4096x4096 + cross 4096x28736), 1 head, d 256, "
+                    "2-D RoPE on q and the 28672 memory keys (64 pointer keys unrotated)",
+        "ms_4_layers": round(total_ms, 4),
+        "self_us": round(self_ms * 1e3, 2), "cross_us": round(cross_ms * 1e3, 2),
+        "tflops": round(4 * (f_self + f_cross) / (total_ms * 1e-3) / 1e12, 1),
+        "self_tflops": round(f_self / (self_ms * 1e-3) / 1e12, 1),
+        "cross_tflops": round(f_cross / (cross_ms * 1e-3) / 1e12, 1),
+        "frac_of_f16_mfma_peak": round(4 * (f_self + f_cross) / (total_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f16"],
+                                       4),
+        "note": "time includes the key-rotation pass and the key-split combine; flops count attention only",
+    }
+    del layers, ws
+
+    # Grounding DINO-tiny deformable attention, f32: 4 levels of an 800x1333 input, 8 heads x 32, 4 points.
+    shapes = [(100, 167), (50, 84), (25, 42), (13, 21)]
+    s = sum(a * b for a, b in shapes)
+    hh, dd, ll, pp = 8, 32, 4, 4
+    value = torch.randn(1, s, hh, dd, device=dev, generator=g)
+    flat = (ctypes.c_int * 8)(*[x for hw in shapes for x in hw])
+    for name, q in (("encoder", s), ("decoder", 900)):
+        ref = torch.rand(1, q, 1, 1, 1, 2, device=dev, generator=g)
+        wh = torch.tensor([[w_, h_] for h_, w_ in shapes], device=dev, dtype=torch.float32).view(1, 1, 1, ll, 1, 2)
+        off = 2.0 * torch.randn(1, q, hh, ll, pp, 2, device=dev, generator=g)
+        loc = (ref + off / wh).contiguous()
+        attn_w = torch.softmax(torch.randn(1, q, hh, ll * pp, device=dev, generator=g), -1).view(1, q, hh, ll, pp)
+        attn_w = attn_w.contiguous()
+        out = torch.empty(1, q, hh * dd, device=dev)
+
+        def run():
+            check(lib, lib.sam_hip_deform_attn(value.data_ptr(), loc.data_ptr(), attn_w.data_ptr(), out.data_ptr(), 0,
+                                               1, s, q, hh, dd, ll, pp, flat, sp))
+
+        ms = timer.avg_ms(run, 50)
+        nbytes = 4.0 * (s * hh * dd + 3 * q * hh * ll * pp + q * hh * dd)
+        res[f"dino_deform_{name}_f32"] = {
+            "workload": f"Grounding DINO-tiny deformable attention, {q} queries over {s} values, 8 heads x 32, "
+                        "4 levels x 4 points",
+            "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+
+    # SAM ViT-B encoder attention layers, f32 (12 heads x 64): window 300 x 14x14, global 12 x 64x64.
+    for name, bh, hw in (("window", 300, 14), ("global", 12, 64)):
+        n = hw * hw
+        q = torch.randn(bh, n, 64, device=dev, generator=g)
+        kt = torch.randn(bh, 64, n, device=dev, generator=g)
+        v = torch.randn(bh, n, 64, device=dev, generator=g)
+        table = 0.02 * torch.randn(2 * (2 * hw - 1), 64, device=dev, generator=g)
+        out = torch.empty_like(q)
+
+        def run():
+            check(lib, lib.sam_hip_attn_relpos(q.data_ptr(), kt.data_ptr(), v.data_ptr(), table.data_ptr(),
+                                               out.data_ptr(), 0, bh, hw, hw, 64, 0.125, sp))
+
+        ms = timer.avg_ms(run, 20)
+        f = flops(bh, n, 64)
+        res[f"vit_b_{name}_f32"] = {
+            "workload": f"SAM ViT-B {name} attention layer, f32, {bh} x {hw}x{hw}, hd 64",
+            "us": round(ms * 1e3, 2), "tflops": round(f / (ms * 1e-3) / 1e12, 2),
+            "frac_of_f32_peak": round(f / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f32"], 4),
+        }
+    return res
+
+
+def copy_probe(torch):
+    """A device-to-device copy of 256 MiB, five times: reads and writes 256 MiB per launch, the known
+    byte count that scales the FETCH_SIZE / WRITE_SIZE counters."""
+    dev = torch.device("cuda:0")
+    a = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": a.numel() * 4, "launches": 5}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -108,9 +268,13 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.copy_probe:
+        copy_probe(torch)
+        return
+
     import sam_hip
 
-    sam_hip.load()
+    lib = sam_hip.load()
     dev = torch.device("cuda:0")
     dt = {"f16": torch.float16, "bf16": torch.bfloat16}[args.dtype]
     g = torch.Generator(device=dev).manual_seed(0)
@@ -124,17 +288,14 @@ def main():
         out = torch.empty_like(q)
         layers.append((bh, h, w, q, kt, v, table, out))
     scale = HD ** -0.5
-    lib = sam_hip.load()
-    code = {"f16": 1, "bf16": 2}[args.dtype]
+    code = CODE[args.dtype]
     stream = torch.cuda.current_stream(dev)
-    sp = sam_hip._vp(stream.cuda_stream)
+    sp = ctypes.c_void_p(stream.cuda_stream)
 
     def launch(L):
         bh, h, w, q, kt, v, table, out = L
-        rc = lib.sam_hip_attn_relpos(q.data_ptr(), kt.data_ptr(), v.data_ptr(), table.data_ptr(), out.data_ptr(),
-                                     code, bh, h, w, HD, scale, sp)
-        if rc:
-            raise sam_hip.SamHipError(lib.sam_hip_last_error().decode())
+        check(lib, lib.sam_hip_attn_relpos(q.data_ptr(), kt.data_ptr(), v.data_ptr(), table.data_ptr(),
+                                           out.data_ptr(), code, bh, h, w, HD, scale, sp))
 
     keep = {"all": lambda i: True, "global": lambda i: i in GLOBAL_LAYERS,
             "window": lambda i: i not in GLOBAL_LAYERS}[args.layers]
@@ -143,20 +304,15 @@ def main():
         for i, L in enumerate(layers):
             if not keep(i):
                 continue
-            if ev is not None and i in GLOBAL_LAYERS:
-                ev[0].append(torch.cuda.Event(enable_timing=True))
-                ev[1].append(torch.cuda.Event(enable_timing=True))
-                ev[0][-1].record(stream)
+            if ev is None:
                 launch(L)
-                ev[1][-1].record(stream)
-            elif ev is not None:
-                ev[2].append(torch.cuda.Event(enable_timing=True))
-                ev[3].append(torch.cuda.Event(enable_timing=True))
-                ev[2][-1].record(stream)
-                launch(L)
-                ev[3][-1].record(stream)
-            else:
-                launch(L)
+                continue
+            k = 0 if i in GLOBAL_LAYERS else 2
+            ev[k].append(torch.cuda.Event(enable_timing=True))
+            ev[k + 1].append(torch.cuda.Event(enable_timing=True))
+            ev[k][-1].record(stream)
+            launch(L)
+            ev[k + 1][-1].record(stream)
 
     for _ in range(args.warmup):
         step()
@@ -214,7 +370,7 @@ def main():
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4),
-            "traffic": traffic_from_profiles(),
+            "traffic": traffic_from_profiles() if args.batch == 1 else None,
         },
         "global_layer_us": round(glob_ms * 1e3, 2),
         "window_layer_us": round(win_ms * 1e3, 2),
@@ -222,6 +378,8 @@ def main():
         "window_layer_hbm_frac": round(win_gbs / HBM_PEAK_GBS, 4),
         "encoder_tflops": round(total_flops / (ms_step * 1e-3) / 1e12, 1),
     }
+    if not args.no_secondary:
+        line["secondary"] = secondary(torch, sam_hip, lib, dev, sp, Timer(torch, stream))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
