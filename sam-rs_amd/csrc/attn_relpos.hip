@@ -46,8 +46,7 @@ template <> struct KChunk<2> { typedef unsigned int type; };
 template <> struct KChunk<1> { typedef unsigned short type; };
 
 constexpr float kRescaleSlack = 8.0f;
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
+constexpr int kMaxWaves = 8;
 
 // LDS strides in elements. A transpose read has each group of 16 lanes fetch 4 rows x 4 chunks of
 // 8 bytes; the row strides below move consecutive rows by 8 (or 24) banks of the 32.
@@ -71,13 +70,14 @@ __device__ __forceinline__ int xcd_major_block(int i, int total) {
 
 // NBUF = 4: resident (needs ntiles <= 4). FULL: every chunk of every tile is in range (hd == HDP,
 // W == padded row width, H a multiple of the rows per tile), so the range checks compile away.
-template <typename T, int HDP, int MODE, int VK, bool POS, int NBUF, bool FULL>
-__global__ __launch_bounds__(kThreads) void attn_relpos_kernel(const T* __restrict__ q, const T* __restrict__ kt,
+template <typename T, int HDP, int MODE, int VK, bool POS, int NBUF, bool FULL, int NWV>
+__global__ __launch_bounds__(NWV * 64) void attn_relpos_kernel(const T* __restrict__ q, const T* __restrict__ kt,
                                                               const T* __restrict__ v, const T* __restrict__ table,
                                                               T* __restrict__ out, int hd, int H, int W,
                                                               float scale, int qblocks) {
   typedef KeyGeom<MODE> G;
   typedef typename Vec<T>::x8 X8;
+  constexpr int kWaves = NWV, kThreads = NWV * 64;
   constexpr bool RES = NBUF > 2;
   constexpr bool kSplitP = __is_same(T, bf16);
   constexpr int KS = HDP / 16;
@@ -461,42 +461,42 @@ __global__ __launch_bounds__(kThreads) void attn_relpos_kernel(const T* __restri
 
 // ---------------------------------------------------------------------------------------------- launch
 
-template <typename T, int HDP, int MODE, int VK, bool POS, int NBUF, bool FULL>
+template <typename T, int HDP, int MODE, int VK, bool POS, int NBUF, bool FULL, int NWV>
 static hipError_t launch_attn(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                               int hd, int h, int w, float scale, hipStream_t stream) {
   const int rows = h > w ? h : w;
-  const size_t lds = tiles_lds_bytes<T, HDP, NBUF>() + (size_t)kWaves * (rows + 1) * 32 * sizeof(float);
-  auto kern = attn_relpos_kernel<T, HDP, MODE, VK, POS, NBUF, FULL>;
+  const size_t lds = tiles_lds_bytes<T, HDP, NBUF>() + (size_t)NWV * (rows + 1) * 32 * sizeof(float);
+  auto kern = attn_relpos_kernel<T, HDP, MODE, VK, POS, NBUF, FULL, NWV>;
   static bool attr_set = false;  // one-time opt-in to more than 64 KB of dynamic LDS
   if (!attr_set) {
-    const size_t max_lds = tiles_lds_bytes<T, HDP, NBUF>() + (size_t)kWaves * 65 * 32 * sizeof(float);
+    const size_t max_lds = tiles_lds_bytes<T, HDP, NBUF>() + (size_t)NWV * 65 * 32 * sizeof(float);
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)(max_lds < 163840 ? max_lds : 163840));
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   const int n = h * w;
-  const int qblocks = (n + kWaves * 32 - 1) / (kWaves * 32);  // 256 queries per workgroup
+  const int qblocks = (n + NWV * 32 - 1) / (NWV * 32);  // NWV * 32 queries per workgroup
   const long blocks = (long)bh * qblocks;
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kThreads), lds, stream, (const T*)q, (const T*)kt,
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NWV * 64), lds, stream, (const T*)q, (const T*)kt,
                      (const T*)v, (const T*)table, (T*)out, hd, h, w, scale, qblocks);
   return hipGetLastError();
 }
 
-template <typename T, int HDP, int MODE, int NBUF>
+template <typename T, int HDP, int MODE, int NBUF, int NWV>
 static hipError_t pick_vk(const void* q, const void* kt, const void* v, const void* table, void* out, int bh, int hd,
                           int h, int w, float scale, hipStream_t stream) {
   const int n = h * w;
   if (!(scale > 0.f))  // the generic path: any scale, any alignment
-    return launch_attn<T, HDP, MODE, 1, false, NBUF, false>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+    return launch_attn<T, HDP, MODE, 1, false, NBUF, false, NWV>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   if (w % 8 == 0 && n % 8 == 0) {
     if (NBUF == 2 && hd == HDP && w == KeyGeom<MODE>::WP && h % KeyGeom<MODE>::RPT == 0)
-      return launch_attn<T, HDP, MODE, 8, true, NBUF, true>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
-    return launch_attn<T, HDP, MODE, 8, true, NBUF, false>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+      return launch_attn<T, HDP, MODE, 8, true, NBUF, true, NWV>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+    return launch_attn<T, HDP, MODE, 8, true, NBUF, false, NWV>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   }
   if (w % 2 == 0 && n % 2 == 0)
-    return launch_attn<T, HDP, MODE, 2, true, NBUF, false>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
-  return launch_attn<T, HDP, MODE, 1, true, NBUF, false>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+    return launch_attn<T, HDP, MODE, 2, true, NBUF, false, NWV>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  return launch_attn<T, HDP, MODE, 1, true, NBUF, false, NWV>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
 }
 
 template <typename T, int HDP, int MODE>
@@ -504,10 +504,10 @@ static hipError_t pick_nbuf(const void* q, const void* kt, const void* v, const 
                             int h, int w, float scale, hipStream_t stream) {
   const int ntiles = (h + KeyGeom<MODE>::RPT - 1) / KeyGeom<MODE>::RPT;
   const int rows = h > w ? h : w;
-  const size_t res_lds = tiles_lds_bytes<T, HDP, 4>() + (size_t)kWaves * (rows + 1) * 32 * sizeof(float);
+  const size_t res_lds = tiles_lds_bytes<T, HDP, 4>() + (size_t)kMaxWaves * (rows + 1) * 32 * sizeof(float);
   if (ntiles <= 4 && res_lds <= 163840)
-    return pick_vk<T, HDP, MODE, 4>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
-  return pick_vk<T, HDP, MODE, 2>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+    return pick_vk<T, HDP, MODE, 4, kMaxWaves>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  return pick_vk<T, HDP, MODE, 2, kMaxWaves>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
 }
 
 template <typename T, int HDP>
@@ -529,8 +529,14 @@ static hipError_t pick_hd(const void* q, const void* kt, const void* v, const vo
 }
 
 // Shape limits are checked by the caller (sam_hip_abi.cpp): 1 <= h, w <= 64, hd % 8 == 0, hd <= 128.
+bool attn_relpos_window(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
+                        int hd, int h, int w, float scale, hipStream_t stream, hipError_t* err);
+
 hipError_t attn_relpos_half(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out,
                             int bh, int hd, int h, int w, float scale, hipStream_t stream) {
+  hipError_t e;
+  // windowed grids (the 14x14 SAM windows): the persistent kernel of attn_relpos_win.hip
+  if (attn_relpos_window(dtype, q, kt, v, table, out, bh, hd, h, w, scale, stream, &e)) return e;
   if (dtype == kF16) return pick_hd<f16>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   return pick_hd<bf16>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
 }

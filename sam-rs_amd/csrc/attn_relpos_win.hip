@@ -1,0 +1,378 @@
+// Fused rel-pos attention for the 14x14 windows of the SAM ViT (hd 80), f16 / bf16, for gfx950.
+//
+//   out[u, r, :] = softmax_k( scale * q[r] . k[k] + q[r] . Th[i - kh + H-1] + q[r] . Tw[j - kw + W-1] ) . v
+//
+// for every unit u = (batch, window, head), the same arithmetic as attn_relpos.hip (the reference's
+// bmm(q, kT) -> relpos_softmax -> bmm(P, v), sam1/encoder.rs:79-82, kernels.rs:12-43, 899-924), and
+// the same key loop: tiles of 4 grid rows padded to 16 columns, S^T = K . Q^T on v_mfma_f32_32x32x16
+// with the Rw bias as the initial accumulator and the Rh bias one value per 32-key block (both from a
+// Q . T^T prologue on the MFMA, scattered along the diagonal band in a wave-private scratch), online
+// exp2 softmax with a lazy rescale, O^T = V^T . P^T with P taken straight from the S^T accumulators.
+//
+// What differs is how a window (196 tokens: 31 KB each of q, kT, v) gets into LDS. One workgroup of
+// 8 waves (one block of 32 queries each) per unit:
+//   * the q rows, the table and all four K/V tiles are requested at once with LDS DMA (global_load_lds),
+//     so no registers stage them; the kernel issues no other loads, so the only waits on memory are
+//     its own;
+//   * each tile is waited for on its own (s_waitcnt vmcnt counts this wave's DMAs still in flight,
+//     which complete in issue order, then a barrier): tile 0's S^T starts while tiles 1..3 are still
+//     arriving, and the q fragments and table arrive first of all;
+//   * kT tiles are stored [d][64 slots] with the 8-byte chunks of each row XOR-swizzled by the row's
+//     low bits, so the transpose reads (ds_read_b64_tr_b16) of four consecutive rows hit disjoint
+//     banks; V tiles are [64 slots][80] (160-byte rows: consecutive rows 8 banks apart). The O^T rows
+//     80..95 read past a slot's 80 columns and are discarded; the softmax denominator is summed on the
+//     VALU.
+// Padding keys (columns >= W, rows >= H) and padding table rows read valid data of the same tensor:
+// the keys' bias is -inf (P = 0), and the table rows' products are never scattered.
+// Limits (checked by the dispatcher): 13 <= H <= 16 (4 key tiles), W <= 16 and even, hd 80, scale > 0.
+#include "relpos_geom.hpp"
+
+namespace samhip {
+
+namespace win {
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kHD = 80;        // head dim of this kernel
+constexpr int kKS = kHD / 16;  // k-steps of S^T = K Q^T
+constexpr int kMBO = 3;        // 32-row blocks of O^T (rows 80..95 are not stored)
+constexpr int kTiles = 4;      // key tiles per unit
+constexpr int kTile = kHD * 64;                // elements of a kT tile [d][64] and of a V tile [64][80]
+constexpr int kDma = kTile * 2 / 256 / kWaves; // 4-byte DMAs (256 bytes each) per wave per tile: 5
+constexpr int kTRows = 64;                     // table rows in LDS: Th at [0, 32), Tw at [32, 64)
+constexpr int kTDma = kTRows * kHD * 2 / 256 / kWaves;  // 5
+constexpr int kRhsRows = 17;                   // per-wave bias scratch rows (16 + one junk row)
+constexpr float kSlack = 8.0f;
+static_assert(kTile * 2 % (256 * kWaves) == 0 && kTRows * kHD * 2 % (256 * kWaves) == 0, "DMA split");
+
+constexpr int kQDma = 4;                       // 16-byte DMAs (1 KB each) of the q rows per wave
+// kT, then V, then the q rows, then the table, then the per-wave scratch; the V tiles are followed by
+// 16 spare elements for the discarded O^T rows of the last slot.
+constexpr int kVOff = kTiles * kTile;
+constexpr int kQOff = kVOff + kTiles * kTile + 16;
+constexpr int kTOff = kQOff + kWaves * kQDma * 512;
+constexpr size_t kLdsBytes = (size_t)(kTOff + kTRows * kHD) * 2 + (size_t)kWaves * kRhsRows * 32 * sizeof(float);
+
+// Chunk swizzle of kT rows: 8-byte chunk c of row d is stored at c ^ kswz(d & 3).
+__host__ __device__ constexpr int kswz(int r) { return 2 * (r & 1) + 8 * (r >> 1); }
+
+}  // namespace win
+
+// LDS DMA (global_load_lds_dword): lane l's 4 bytes at base + off land at LDS byte address lds + 4 l.
+// base is wave-uniform (SGPRs), off this lane's byte offset. Issued through inline asm so that the
+// compiler adds no waits of its own before later LDS reads (it cannot tell the regions apart); the
+// kernel waits explicitly with wait_vm and a barrier. M0 is written here and used by nothing else in
+// this kernel (gfx950 LDS instructions do not read it), hence the clobber.
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma4(const void* base, unsigned off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+// The same with 16 bytes a lane (lds + 16 l).
+__device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(size_t)(const __attribute__((address_space(3))) char*)(p);
+}
+
+// Waits until at most N of this wave's vector-memory operations are outstanding (they complete in
+// issue order), i.e. everything issued before the last N is done.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <typename T>
+__global__ __launch_bounds__(win::kThreads) void attn_relpos_win_kernel(const T* __restrict__ q,
+                                                                       const T* __restrict__ kt,
+                                                                       const T* __restrict__ v,
+                                                                       const T* __restrict__ table,
+                                                                       T* __restrict__ out, int H, int W,
+                                                                       float scale) {
+  using namespace win;
+  typedef KeyGeom<kPair> KG;
+  typedef typename Vec<T>::x8 X8;
+  constexpr bool kSplitP = __is_same(T, bf16);
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  T* kring = reinterpret_cast<T*>(smem);
+  T* vring = kring + kVOff;
+  T* tb = kring + kTOff;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: DMA destinations derive from it
+  float* rhs = reinterpret_cast<float*>(tb + kTRows * kHD) + wave * kRhsRows * 32;
+  const unsigned lds0 = lds_addr(smem);
+
+  const int N = H * W;
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 31, hh = lane >> 5;
+  const int g = lane >> 4, gi = lane & 15;
+  const long unit_elems = (long)N * kHD;
+  const long u = blockIdx.x;
+  const int qidx = wave * 32 + n;
+  const bool qvalid = qidx < N;
+  const int qi = qvalid ? qidx / W : 0, qj = qvalid ? qidx % W : 0;
+  const float sc = scale * kLog2e;
+
+  // ---- 1. the q rows of the unit into LDS ([196][80], rows past N read row 0)
+  {
+    const char* base = reinterpret_cast<const char*>(q + u * unit_elems);
+#pragma unroll
+    for (int p = 0; p < kQDma; ++p) {
+      const int i = wave * kQDma + p;  // DMA i covers 16-byte chunks 64 i + lane
+      const int c = i * 64 + lane;
+      const int row = c / (kHD / 8), col = (c % (kHD / 8)) * 8;
+      dma16(base, (unsigned)(sizeof(T) * (row < N ? row * kHD + col : 0)), lds0 + (kQOff + i * 512) * 2);
+    }
+  }
+  // ---- 2. the table: LDS row r < 32 is Th row r, row 32 + r is Tw row r (rows past the end read row 0)
+  {
+    const char* base = reinterpret_cast<const char*>(table);
+#pragma unroll
+    for (int p = 0; p < kTDma; ++p) {
+      const int i = wave * kTDma + p;    // DMA i covers LDS elements [128 i, 128 i + 128)
+      const int e = i * 128 + 2 * lane;  // element of the [64][80] table image
+      const int r = e / kHD, col = e % kHD;
+      const int src = r < 32 ? (r < 2 * H - 1 ? r : 0) : (r - 32 < 2 * W - 1 ? 2 * H - 1 + r - 32 : 0);
+      dma4(base, (unsigned)(sizeof(T) * (src * kHD + col)), lds0 + (kTOff + i * 128) * 2);
+    }
+  }
+  // ---- 3. the four K/V tiles
+  {
+    const char* kb = reinterpret_cast<const char*>(kt + u * unit_elems);
+    const char* vb = reinterpret_cast<const char*>(v + u * unit_elems);
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+#pragma unroll
+      for (int p = 0; p < kDma; ++p) {
+        // kT: DMA i covers rows 2i, 2i + 1 of the tile; this lane's slot pair sits at swizzled position
+        // 2 * (lane & 31) of row d = 2i + hh
+        const int i = wave * kDma + p;
+        const int d = 2 * i + hh;
+        const int pos = 2 * (lane & 31);
+        const int slot = (((pos >> 2) ^ kswz(d & 3)) << 2) + (pos & 3);
+        const int row = 4 * t + (slot >> 4), kap = slot & 15;
+        const bool ok = kap < W && row < H;
+        dma4(kb, (unsigned)(sizeof(T) * (d * N + (ok ? row * W + kap : 0))), lds0 + (t * kTile + i * 128) * 2);
+      }
+#pragma unroll
+      for (int p = 0; p < kDma; ++p) {
+        // V: DMA i covers elements [128 i, 128 i + 128) of the [64 slots][80] tile
+        const int i = wave * kDma + p;
+        const int e = i * 128 + 2 * lane;
+        const int slot = e / kHD, col = e % kHD;
+        const int row = 4 * t + (slot >> 4), kap = slot & 15;
+        const bool ok = kap < W && row < H;
+        dma4(vb, (unsigned)(sizeof(T) * ((ok ? (row * W + kap) * kHD : 0) + col)),
+             lds0 + (kVOff + t * kTile + i * 128) * 2);
+      }
+    }
+  }
+
+  // per-lane constant parts of the transpose-read addresses
+  // kT (A operand of S^T): source lane (4*s + c) of group g reads row 8*(g>>1) + s (+16*k, +4), the 4
+  // slots slot(mb, 16*(g&1) + 4*c); the row's low bits are s, so the swizzle is lane constant
+  int koff[2];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    const int d = 8 * (g >> 1) + (gi >> 2);
+    const int slot = KG::slot(mb, 16 * (g & 1) + 4 * (gi & 3));
+    koff[mb] = d * 64 + (((slot >> 2) ^ kswz(d & 3)) << 2);
+  }
+  // V^T (A operand of O^T): source lane (4*s + c) reads the slot of key 16*(w4&1) + 8*r + 4*(g>>1) + s of
+  // block w4>>1, columns 32*ob + 16*(g&1) + 4*c .. +3
+  int voff[4][2];
+#pragma unroll
+  for (int w4 = 0; w4 < 4; ++w4)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int ms = 16 * (w4 & 1) + 8 * r + 4 * (g >> 1) + (gi >> 2);
+      voff[w4][r] = KG::slot(w4 >> 1, ms) * kHD + 16 * (g & 1) + 4 * (gi & 3);
+    }
+  auto wave_sync = [&]() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  // ---- 4. the bias (q and the table have landed: 4 tiles of DMAs may still be in flight)
+  wait_vm<kTiles * 2 * kDma>();
+  __syncthreads();
+  // this lane's q fragments (B operand of S^T = K Q^T): Q[query][16*s + 8*hh + j]
+  X8 qf[kKS];
+#pragma unroll
+  for (int s = 0; s < kKS; ++s)
+    qf[s] = *reinterpret_cast<const X8*>(kring + kQOff + (qvalid ? qidx : 0) * kHD + 16 * s + 8 * hh);
+  f32x16 cinit;
+  float rh[kTiles][2];
+  {
+    f32x16 gh = f32x16{}, gw = f32x16{};
+#pragma unroll
+    for (int s = 0; s < kKS; ++s) {
+      const X8 ah = *reinterpret_cast<const X8*>(tb + n * kHD + 16 * s + 8 * hh);
+      const X8 aw = *reinterpret_cast<const X8*>(tb + (32 + n) * kHD + 16 * s + 8 * hh);
+      gh = mma32(ah, qf[s], gh);
+      gw = mma32(aw, qf[s], gw);
+    }
+    // Rw: a lane's key columns are e = 0..15 in every 32-key block, so cinit[e] = Rw[e] / sc
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int rr = 8 * (e >> 2) + 4 * hh + (e & 3);
+      const int kw = qj + W - 1 - rr;
+      const bool ok = rr < 2 * W - 1 && kw >= 0 && kw < W;
+      rhs[(ok ? kw : 16) * 32 + n] = gw[e] * kLog2e;
+    }
+    wave_sync();
+    const float inv_sc = 1.f / sc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float x = rhs[e * 32 + n];
+      cinit[e] = e < W ? x * inv_sc : -INFINITY;
+    }
+    wave_sync();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int rr = 8 * (e >> 2) + 4 * hh + (e & 3);
+      const int kh = qi + H - 1 - rr;
+      const bool ok = rr < 2 * H - 1 && kh >= 0 && kh < H;
+      rhs[(ok ? kh : 16) * 32 + n] = gh[e] * kLog2e;
+    }
+    wave_sync();
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const int row = 4 * t + 2 * mb + hh;  // < 16
+        const float x = rhs[row * 32 + n];
+        rh[t][mb] = row < H ? x : -INFINITY;
+      }
+  }
+
+  // ---- 5. key loop: tile t as soon as its DMAs have landed
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 o[kMBO];
+#pragma unroll
+  for (int ob = 0; ob < kMBO; ++ob) o[ob] = f32x16{};
+  auto tile = [&](int t) {
+    f32x16 s[2];
+    const T* kb = kring + t * kTile;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int k = 0; k < kKS; ++k) {
+        const T* p = kb + koff[mb] + 16 * k * 64;
+        const X8 a = join8<T>(lds_read_tr16(p), lds_read_tr16(p + 4 * 64));
+        s[mb] = mma32(a, qf[k], k == 0 ? cinit : s[mb]);
+      }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      float mm = s[mb][0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) mm = fmaxf(mm, s[mb][e]);
+      mt = fmaxf(mt, fmaf(mm, sc, rh[t][mb]));
+    }
+    mt = max_with_partner32(mt);
+    if (wave_any(mt > m_run + kSlack)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = exp2_fast(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int ob = 0; ob < kMBO; ++ob) o[ob] *= alpha;
+      m_run = m_new;
+    }
+    float c[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) c[mb] = rh[t][mb] - m_run;
+    X8 b[4], blo[4];
+    float lsum = 0.f;
+#pragma unroll
+    for (int w4 = 0; w4 < 4; ++w4) {
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pv[e] = exp2_fast(fmaf(s[w4 >> 1][8 * (w4 & 1) + e], sc, c[w4 >> 1]));
+        lsum += pv[e];
+      }
+      b[w4] = pack8(pv, (X8*)nullptr);
+      if (kSplitP) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] -= to_f32(b[w4][e]);
+        blo[w4] = pack8(pv, (X8*)nullptr);
+      }
+    }
+    l_run += lsum;
+    const T* vb = vring + t * kTile;
+#pragma unroll
+    for (int w4 = 0; w4 < 4; ++w4) {
+#pragma unroll
+      for (int ob = 0; ob < kMBO; ++ob) {
+        const X8 a = join8<T>(lds_read_tr16(vb + voff[w4][0] + 32 * ob), lds_read_tr16(vb + voff[w4][1] + 32 * ob));
+        o[ob] = mma32(a, b[w4], o[ob]);
+        if (kSplitP) o[ob] = mma32(a, blo[w4], o[ob]);
+      }
+    }
+  };
+  wait_vm<3 * 2 * kDma>();
+  __syncthreads();
+  tile(0);
+  wait_vm<2 * 2 * kDma>();
+  __syncthreads();
+  tile(1);
+  wait_vm<1 * 2 * kDma>();
+  __syncthreads();
+  tile(2);
+  wait_vm<0>();
+  __syncthreads();
+  tile(3);
+
+  // ---- 6. normalise and store: lane holds O^T[32*ob + 8*a + 4*hh + b][query n]
+  const float inv = 1.f / sum_with_partner32(l_run);
+  if (qvalid) {
+    T* orow = out + u * unit_elems + qidx * kHD;
+#pragma unroll
+    for (int ob = 0; ob < kMBO; ++ob)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        if (32 * ob + 8 * a < kHD) {
+          typename Vec<T>::x4 w4;
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb) w4[bb] = from_f32<T>(o[ob][4 * a + bb] * inv);
+          *reinterpret_cast<typename Vec<T>::x4*>(orow + 32 * ob + 8 * a + 4 * hh) = w4;
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- launch
+
+template <typename T>
+static hipError_t launch_win(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
+                             int h, int w, float scale, hipStream_t stream) {
+  auto kern = attn_relpos_win_kernel<T>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e =
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)win::kLdsBytes);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)bh), dim3(win::kThreads), win::kLdsBytes, stream, (const T*)q,
+                     (const T*)kt, (const T*)v, (const T*)table, (T*)out, h, w, scale);
+  return hipGetLastError();
+}
+
+// The SAM windows (13 <= H <= 16 so a unit is exactly 4 key tiles, W <= 16 even, hd 80, scale > 0);
+// returns false (nothing launched) for shapes it does not take.
+bool attn_relpos_window(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
+                        int hd, int h, int w, float scale, hipStream_t stream, hipError_t* err) {
+  if (hd != win::kHD || h < 13 || h > 16 || w > 16 || w % 2 != 0 || !(scale > 0.f)) return false;
+  *err = dtype == kF16 ? launch_win<f16>(q, kt, v, table, out, bh, h, w, scale, stream)
+                       : launch_win<bf16>(q, kt, v, table, out, bh, h, w, scale, stream);
+  return true;
+}
+
+}  // namespace samhip
