@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "libsam_hip.so")
 
 SOURCES = [
     "attn_relpos.hip",
-    "attn_relpos_win.hip",
+    "attn_relpos_win.hip", "attn_relpos_glob.hip",
     "attn_relpos_f32.hip",
     "deform_attn.hip",
     "relpos_softmax.hip",

@@ -531,12 +531,16 @@ static hipError_t pick_hd(const void* q, const void* kt, const void* v, const vo
 // Shape limits are checked by the caller (sam_hip_abi.cpp): 1 <= h, w <= 64, hd % 8 == 0, hd <= 128.
 bool attn_relpos_window(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                         int hd, int h, int w, float scale, hipStream_t stream, hipError_t* err);
+bool attn_relpos_global(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
+                        int hd, int h, int w, float scale, hipStream_t stream, hipError_t* err);
 
 hipError_t attn_relpos_half(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out,
                             int bh, int hd, int h, int w, float scale, hipStream_t stream) {
   hipError_t e;
-  // windowed grids (the 14x14 SAM windows): the persistent kernel of attn_relpos_win.hip
+  // windowed grids (the 14x14 SAM windows): attn_relpos_win.hip; the 64-column global grid:
+  // attn_relpos_glob.hip; every other shape: the general kernel below
   if (attn_relpos_window(dtype, q, kt, v, table, out, bh, hd, h, w, scale, stream, &e)) return e;
+  if (attn_relpos_global(dtype, q, kt, v, table, out, bh, hd, h, w, scale, stream, &e)) return e;
   if (dtype == kF16) return pick_hd<f16>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   return pick_hd<bf16>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
 }

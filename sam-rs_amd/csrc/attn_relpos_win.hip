@@ -25,6 +25,7 @@
 // Padding keys (columns >= W, rows >= H) and padding table rows read valid data of the same tensor:
 // the keys' bias is -inf (P = 0), and the table rows' products are never scattered.
 // Limits (checked by the dispatcher): 13 <= H <= 16 (4 key tiles), W <= 16 and even, hd 80, scale > 0.
+#include "lds_dma.hpp"
 #include "relpos_geom.hpp"
 
 namespace samhip {
@@ -57,33 +58,6 @@ constexpr size_t kLdsBytes = (size_t)(kTOff + kTRows * kHD) * 2 + (size_t)kWaves
 __host__ __device__ constexpr int kswz(int r) { return 2 * (r & 1) + 8 * (r >> 1); }
 
 }  // namespace win
-
-// LDS DMA (global_load_lds_dword): lane l's 4 bytes at base + off land at LDS byte address lds + 4 l.
-// base is wave-uniform (SGPRs), off this lane's byte offset. Issued through inline asm so that the
-// compiler adds no waits of its own before later LDS reads (it cannot tell the regions apart); the
-// kernel waits explicitly with wait_vm and a barrier. M0 is written here and used by nothing else in
-// this kernel (gfx950 LDS instructions do not read it), hence the clobber.
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma4(const void* base, unsigned off, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
-}
-// The same with 16 bytes a lane (lds + 16 l).
-__device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
-               : "memory", "m0");
-}
-
-__device__ __forceinline__ unsigned lds_addr(const void* p) {
-  return (unsigned)(size_t)(const __attribute__((address_space(3))) char*)(p);
-}
-
-// Waits until at most N of this wave's vector-memory operations are outstanding (they complete in
-// issue order), i.e. everything issued before the last N is done.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 template <typename T>
 __global__ __launch_bounds__(win::kThreads) void attn_relpos_win_kernel(const T* __restrict__ q,

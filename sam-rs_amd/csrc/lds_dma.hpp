@@ -1,0 +1,60 @@
+// LDS DMA helpers for gfx950: global_load_lds (global memory straight into LDS, no registers) and
+// explicit vector-memory waits.
+//
+// The DMAs are issued through inline asm so that the compiler inserts no waits of its own before later
+// LDS reads (it cannot tell which LDS region a DMA writes); a kernel using them issues no other vector
+// loads and waits explicitly with wait_vm, whose count relies on a wave's vector-memory operations
+// completing in issue order. M0 is written by every DMA and read by nothing else in these kernels
+// (gfx950 LDS instructions do not use it), hence the clobber of a register the compiler reserves.
+#pragma once
+#include "common.hpp"
+
+#pragma clang diagnostic ignored "-Winline-asm"
+
+namespace samhip {
+
+// Lane l's 4 bytes at base + off land at LDS byte address lds + 4 l. base is wave-uniform (SGPRs),
+// off this lane's byte offset from it, lds wave-uniform.
+__device__ __forceinline__ void dma4(const void* base, unsigned off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+// The same with 16 bytes a lane (lds + 16 l).
+__device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
+// LDS byte address of a pointer into dynamic shared memory.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(size_t)(const __attribute__((address_space(3))) char*)(p);
+}
+
+// ds_read_b64_tr_b16 (the lane layout of lds_read_tr16) at a byte address of the workgroup's LDS.
+__device__ __forceinline__ i16x4 lds_read_tr16_at(unsigned addr) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(size_t)addr);
+}
+
+// Hides v's value from the optimiser, so that constants added to it later stay instruction offsets
+// instead of being folded into new per-lane base registers.
+__device__ __forceinline__ unsigned opaque(unsigned v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Makes x's current value an input and output of an empty volatile asm statement: the computation of
+// x cannot be moved past this point (a barrier is no obstacle to moving pure arithmetic otherwise).
+template <typename V>
+__device__ __forceinline__ void pin(V& x) {
+  asm volatile("" : "+v"(x));
+}
+
+// Waits until at most N of this wave's vector-memory operations are outstanding, i.e. everything
+// issued before the last N is done.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+}  // namespace samhip
