@@ -365,7 +365,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "attn_relpos_kernel (global 64x64 layer)",
+            "kernel": "attn_relpos_glob_kernel (global 64x64 layer)",
             "achieved": round(achieved, 1),
             "peak": peak,
             "unit": "TFLOP/s",
