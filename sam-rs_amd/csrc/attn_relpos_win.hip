@@ -9,19 +9,22 @@
 // Q . T^T prologue on the MFMA, scattered along the diagonal band in a wave-private scratch), online
 // exp2 softmax with a lazy rescale, O^T = V^T . P^T with P taken straight from the S^T accumulators.
 //
-// What differs is how a window (196 tokens: 31 KB each of q, kT, v) gets into LDS. One workgroup of
-// 8 waves (one block of 32 queries each) per unit:
-//   * the q rows, the table and all four K/V tiles are requested at once with LDS DMA (global_load_lds),
-//     so no registers stage them; the kernel issues no other loads, so the only waits on memory are
-//     its own;
-//   * each tile is waited for on its own (s_waitcnt vmcnt counts this wave's DMAs still in flight,
-//     which complete in issue order, then a barrier): tile 0's S^T starts while tiles 1..3 are still
-//     arriving, and the q fragments and table arrive first of all;
+// A windowed layer is bound by HBM and by latency: a unit is 125 KB of q, kT, v and out for 12 MFLOP,
+// and there are only 400 of them per ViT-H layer. So the kernel is built for overlap between
+// workgroups rather than for a single one:
+//   * a workgroup of 4 waves takes half a unit (query blocks 0-3 or 4-7, one per wave) and needs
+//     70 KB of LDS, so two fit on a CU: one loads while the other computes, and the 800 half units
+//     fill the 512 workgroup slots of the chip in one and a half rounds instead of two full ones;
+//   * all data moves by LDS DMA (global_load_lds): the q rows, the table and tile 0 are requested at
+//     once, q into ring buffer 1 and the table into buffer 2, which tiles 1 and 2 take over once the
+//     bias prologue has read them; tile 3 then goes into buffer 0. The two halves of a unit are
+//     adjacent workgroups on one XCD, so the second half's K and V come from L2;
+//   * each wave waits only for its own DMAs of what it needs next (s_waitcnt vmcnt: a wave's vector
+//     memory operations complete in issue order), then one barrier publishes everyone's share;
 //   * kT tiles are stored [d][64 slots] with the 8-byte chunks of each row XOR-swizzled by the row's
 //     low bits, so the transpose reads (ds_read_b64_tr_b16) of four consecutive rows hit disjoint
-//     banks; V tiles are [64 slots][80] (160-byte rows: consecutive rows 8 banks apart). The O^T rows
-//     80..95 read past a slot's 80 columns and are discarded; the softmax denominator is summed on the
-//     VALU.
+//     banks; V tiles are [64 slots][80]. The O^T rows 80..95 read past a slot's 80 columns and are
+//     discarded; the softmax denominator is summed on the VALU.
 // Padding keys (columns >= W, rows >= H) and padding table rows read valid data of the same tensor:
 // the keys' bias is -inf (P = 0), and the table rows' products are never scattered.
 // Limits (checked by the dispatcher): 13 <= H <= 16 (4 key tiles), W <= 16 and even, hd 80, scale > 0.
@@ -32,35 +35,49 @@ namespace samhip {
 
 namespace win {
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kHD = 80;        // head dim of this kernel
 constexpr int kKS = kHD / 16;  // k-steps of S^T = K Q^T
 constexpr int kMBO = 3;        // 32-row blocks of O^T (rows 80..95 are not stored)
 constexpr int kTiles = 4;      // key tiles per unit
-constexpr int kTile = kHD * 64;                // elements of a kT tile [d][64] and of a V tile [64][80]
-constexpr int kDma = kTile * 2 / 256 / kWaves; // 4-byte DMAs (256 bytes each) per wave per tile: 5
-constexpr int kTRows = 64;                     // table rows in LDS: Th at [0, 32), Tw at [32, 64)
-constexpr int kTDma = kTRows * kHD * 2 / 256 / kWaves;  // 5
-constexpr int kRhsRows = 17;                   // per-wave bias scratch rows (16 + one junk row)
+constexpr int kRing = 3;       // tile buffers
+constexpr int kTile = kHD * 64;                  // elements of a kT tile [d][64] and of a V tile [64][80]
+constexpr int kKDma = kTile * 2 / 256 / kWaves;  // 4-byte DMAs of a kT tile per wave: 10
+constexpr int kVDma = 3;                         // 1 KB units of a V tile per wave (12 >= 10: 2 repeats)
+constexpr int kTDma = kKDma + kVDma;             // DMAs per wave per tile
+constexpr int kQRows = kWaves * 32;              // q rows of a half unit
+constexpr int kQDma = kQRows * kHD * 2 / 1024 / kWaves;  // 1 KB units of q per wave: 5
+constexpr int kTRows = 64;                       // table rows in LDS: Th at [0, 32), Tw at [32, 64)
+constexpr int kTbDma = 3;                        // 1 KB units of the table per wave (12 >= 10: 2 repeats)
+constexpr int kRhsRows = 17;                     // per-wave bias scratch rows (16 + one junk row)
 constexpr float kSlack = 8.0f;
-static_assert(kTile * 2 % (256 * kWaves) == 0 && kTRows * kHD * 2 % (256 * kWaves) == 0, "DMA split");
+static_assert(kTile * 2 % (256 * kWaves) == 0 && kQRows * kHD * 2 % (1024 * kWaves) == 0, "DMA split");
+static_assert(kTile * 2 <= kVDma * kWaves * 1024 && kTRows * kHD * 2 <= kTbDma * kWaves * 1024, "units");
 
-constexpr int kQDma = 4;                       // 16-byte DMAs (1 KB each) of the q rows per wave
-// kT, then V, then the q rows, then the table, then the per-wave scratch; the V tiles are followed by
-// 16 spare elements for the discarded O^T rows of the last slot.
-constexpr int kVOff = kTiles * kTile;
-constexpr int kQOff = kVOff + kTiles * kTile + 16;
-constexpr int kTOff = kQOff + kWaves * kQDma * 512;
-constexpr size_t kLdsBytes = (size_t)(kTOff + kTRows * kHD) * 2 + (size_t)kWaves * kRhsRows * 32 * sizeof(float);
+// Buffer b is a kT tile at 2 b kTile and a V tile right after it; the last V tile is followed by 16
+// spare elements for the discarded O^T rows of its last slot; then the per-wave scratch. The q rows
+// fill buffer 1 and the table the kT half of buffer 2 until the prologue has read them.
+constexpr int kBuf = 2 * kTile;
+constexpr int kQOff = kBuf;
+constexpr int kTbOff = 2 * kBuf;
+constexpr int kRhsOff = kRing * kBuf + 16;
+constexpr size_t kLdsBytes = (size_t)kRhsOff * 2 + (size_t)kWaves * kRhsRows * 32 * sizeof(float);
+static_assert(kQRows * kHD <= kBuf && kTRows * kHD <= kTile, "staging fits buffers 1 and 2");
+static_assert(2 * kLdsBytes <= 160 * 1024, "two workgroups per CU");
 
 // Chunk swizzle of kT rows: 8-byte chunk c of row d is stored at c ^ kswz(d & 3).
 __host__ __device__ constexpr int kswz(int r) { return 2 * (r & 1) + 8 * (r >> 1); }
 
 }  // namespace win
 
+__device__ __forceinline__ int win_xcd_block(int i, int total) {
+  const int per = total >> 3, rem = total & 7, x = i & 7, j = i >> 3;
+  return x * per + (x < rem ? x : rem) + j;
+}
+
 template <typename T>
-__global__ __launch_bounds__(win::kThreads) void attn_relpos_win_kernel(const T* __restrict__ q,
+__global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const T* __restrict__ q,
                                                                        const T* __restrict__ kt,
                                                                        const T* __restrict__ v,
                                                                        const T* __restrict__ table,
@@ -73,10 +90,9 @@ __global__ __launch_bounds__(win::kThreads) void attn_relpos_win_kernel(const T*
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   T* kring = reinterpret_cast<T*>(smem);
-  T* vring = kring + kVOff;
-  T* tb = kring + kTOff;
+  T* tb = kring + kTbOff;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: DMA destinations derive from it
-  float* rhs = reinterpret_cast<float*>(tb + kTRows * kHD) + wave * kRhsRows * 32;
+  float* rhs = reinterpret_cast<float*>(kring + kRhsOff) + wave * kRhsRows * 32;
   const unsigned lds0 = lds_addr(smem);
 
   const int N = H * W;
@@ -84,66 +100,72 @@ __global__ __launch_bounds__(win::kThreads) void attn_relpos_win_kernel(const T*
   const int n = lane & 31, hh = lane >> 5;
   const int g = lane >> 4, gi = lane & 15;
   const long unit_elems = (long)N * kHD;
-  const long u = blockIdx.x;
-  const int qidx = wave * 32 + n;
+  const int blk = win_xcd_block(blockIdx.x, gridDim.x);
+  const long u = blk >> 1;
+  const int q0 = (blk & 1) * kQRows;  // first query of this half unit
+  const int qidx = q0 + wave * 32 + n;
   const bool qvalid = qidx < N;
   const int qi = qvalid ? qidx / W : 0, qj = qvalid ? qidx % W : 0;
   const float sc = scale * kLog2e;
+  const char* kb = reinterpret_cast<const char*>(kt + u * unit_elems);
+  const char* vb = reinterpret_cast<const char*>(v + u * unit_elems);
 
-  // ---- 1. the q rows of the unit into LDS ([196][80], rows past N read row 0)
+  // This wave's DMAs of K/V tile t into buffer buf (kTDma of them). Slots outside the grid read key 0.
+  auto tile_dma = [&](int t, int buf) {
+#pragma unroll
+    for (int p = 0; p < kKDma; ++p) {
+      // kT: DMA i covers rows 2i, 2i + 1 of the tile; this lane's slot pair sits at swizzled position
+      // 2 * (lane & 31) of row d = 2i + hh (W is even, so a pair is all in or all out)
+      const int i = wave * kKDma + p;
+      const int d = 2 * i + hh;
+      const int pos = 2 * (lane & 31);
+      const int slot = (((pos >> 2) ^ kswz(d & 3)) << 2) + (pos & 3);
+      const int row = 4 * t + (slot >> 4), kap = slot & 15;
+      const bool ok = kap < W && row < H;
+      dma4(kb, (unsigned)(sizeof(T) * (d * N + (ok ? row * W + kap : 0))), lds0 + (buf * kBuf + i * 128) * 2);
+    }
+#pragma unroll
+    for (int p = 0; p < kVDma; ++p) {
+      // V: unit j covers elements [512 j, 512 j + 512) of the [64 slots][80] tile, a lane 8 columns of
+      // one slot; units 10 and 11 repeat units 0 and 1
+      const int j0 = wave + kWaves * p;
+      const int j = j0 < 10 ? j0 : j0 - 10;
+      const int e = j * 512 + 8 * lane;
+      const int slot = e / kHD, col = e % kHD;
+      const int row = 4 * t + (slot >> 4), kap = slot & 15;
+      const bool ok = kap < W && row < H;
+      dma16(vb, (unsigned)(sizeof(T) * ((ok ? (row * W + kap) * kHD : 0) + col)),
+            lds0 + (buf * kBuf + kTile + j * 512) * 2);
+    }
+  };
+
+  // ---- 1. the half unit's q rows, the table and tile 0, all requested at once
   {
     const char* base = reinterpret_cast<const char*>(q + u * unit_elems);
 #pragma unroll
     for (int p = 0; p < kQDma; ++p) {
-      const int i = wave * kQDma + p;  // DMA i covers 16-byte chunks 64 i + lane
-      const int c = i * 64 + lane;
-      const int row = c / (kHD / 8), col = (c % (kHD / 8)) * 8;
-      dma16(base, (unsigned)(sizeof(T) * (row < N ? row * kHD + col : 0)), lds0 + (kQOff + i * 512) * 2);
+      const int i = wave * kQDma + p;  // unit i covers q-image elements [512 i, 512 i + 512)
+      const int e = i * 512 + 8 * lane;
+      const int row = e / kHD, col = e % kHD;
+      const int src = q0 + row;  // queries past the end read query 0
+      dma16(base, (unsigned)(sizeof(T) * ((src < N ? src : 0) * kHD + col)), lds0 + (kQOff + i * 512) * 2);
     }
   }
-  // ---- 2. the table: LDS row r < 32 is Th row r, row 32 + r is Tw row r (rows past the end read row 0)
   {
+    // LDS row r < 32 is Th row r, row 32 + r is Tw row r (rows past the end read row 0); units 10, 11
+    // repeat units 0, 1
     const char* base = reinterpret_cast<const char*>(table);
 #pragma unroll
-    for (int p = 0; p < kTDma; ++p) {
-      const int i = wave * kTDma + p;    // DMA i covers LDS elements [128 i, 128 i + 128)
-      const int e = i * 128 + 2 * lane;  // element of the [64][80] table image
+    for (int p = 0; p < kTbDma; ++p) {
+      const int i0 = wave + kWaves * p;
+      const int i = i0 < 10 ? i0 : i0 - 10;
+      const int e = i * 512 + 8 * lane;
       const int r = e / kHD, col = e % kHD;
       const int src = r < 32 ? (r < 2 * H - 1 ? r : 0) : (r - 32 < 2 * W - 1 ? 2 * H - 1 + r - 32 : 0);
-      dma4(base, (unsigned)(sizeof(T) * (src * kHD + col)), lds0 + (kTOff + i * 128) * 2);
+      dma16(base, (unsigned)(sizeof(T) * (src * kHD + col)), lds0 + (kTbOff + i * 512) * 2);
     }
   }
-  // ---- 3. the four K/V tiles
-  {
-    const char* kb = reinterpret_cast<const char*>(kt + u * unit_elems);
-    const char* vb = reinterpret_cast<const char*>(v + u * unit_elems);
-#pragma unroll
-    for (int t = 0; t < kTiles; ++t) {
-#pragma unroll
-      for (int p = 0; p < kDma; ++p) {
-        // kT: DMA i covers rows 2i, 2i + 1 of the tile; this lane's slot pair sits at swizzled position
-        // 2 * (lane & 31) of row d = 2i + hh
-        const int i = wave * kDma + p;
-        const int d = 2 * i + hh;
-        const int pos = 2 * (lane & 31);
-        const int slot = (((pos >> 2) ^ kswz(d & 3)) << 2) + (pos & 3);
-        const int row = 4 * t + (slot >> 4), kap = slot & 15;
-        const bool ok = kap < W && row < H;
-        dma4(kb, (unsigned)(sizeof(T) * (d * N + (ok ? row * W + kap : 0))), lds0 + (t * kTile + i * 128) * 2);
-      }
-#pragma unroll
-      for (int p = 0; p < kDma; ++p) {
-        // V: DMA i covers elements [128 i, 128 i + 128) of the [64 slots][80] tile
-        const int i = wave * kDma + p;
-        const int e = i * 128 + 2 * lane;
-        const int slot = e / kHD, col = e % kHD;
-        const int row = 4 * t + (slot >> 4), kap = slot & 15;
-        const bool ok = kap < W && row < H;
-        dma4(vb, (unsigned)(sizeof(T) * ((ok ? (row * W + kap) * kHD : 0) + col)),
-             lds0 + (kVOff + t * kTile + i * 128) * 2);
-      }
-    }
-  }
+  tile_dma(0, 0);
 
   // per-lane constant parts of the transpose-read addresses
   // kT (A operand of S^T): source lane (4*s + c) of group g reads row 8*(g>>1) + s (+16*k, +4), the 4
@@ -171,14 +193,14 @@ __global__ __launch_bounds__(win::kThreads) void attn_relpos_win_kernel(const T*
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
 
-  // ---- 4. the bias (q and the table have landed: 4 tiles of DMAs may still be in flight)
-  wait_vm<kTiles * 2 * kDma>();
+  // ---- 2. the bias (q and the table have landed; tile 0 may still be in flight)
+  wait_vm<kTDma>();
   __syncthreads();
   // this lane's q fragments (B operand of S^T = K Q^T): Q[query][16*s + 8*hh + j]
   X8 qf[kKS];
 #pragma unroll
   for (int s = 0; s < kKS; ++s)
-    qf[s] = *reinterpret_cast<const X8*>(kring + kQOff + (qvalid ? qidx : 0) * kHD + 16 * s + 8 * hh);
+    qf[s] = *reinterpret_cast<const X8*>(kring + kQOff + (wave * 32 + n) * kHD + 16 * s + 8 * hh);
   f32x16 cinit;
   float rh[kTiles][2];
   {
@@ -223,27 +245,33 @@ __global__ __launch_bounds__(win::kThreads) void attn_relpos_win_kernel(const T*
         rh[t][mb] = row < H ? x : -INFINITY;
       }
   }
+  __syncthreads();  // everyone has read q and the table: buffers 1 and 2 are free
+  tile_dma(1, 1);
+  tile_dma(2, 2);
 
-  // ---- 5. key loop: tile t as soon as its DMAs have landed
+  // ---- 3. key loop: tile t as soon as its DMAs have landed
   float m_run = -INFINITY, l_run = 0.f;
   f32x16 o[kMBO];
 #pragma unroll
   for (int ob = 0; ob < kMBO; ++ob) o[ob] = f32x16{};
-  auto tile = [&](int t) {
+  // Tile t from buffer buf. NB = 1 when the tile's second 32-key block (grid rows 4t+2, 4t+3) lies
+  // wholly below the grid: its products, exponentials and P.V are skipped.
+  auto tile = [&](int t, int buf, auto nb_c) {
+    constexpr int NB = decltype(nb_c)::value;
     f32x16 s[2];
-    const T* kb = kring + t * kTile;
+    const T* kbuf = kring + buf * kBuf;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < NB; ++mb) {
 #pragma unroll
       for (int k = 0; k < kKS; ++k) {
-        const T* p = kb + koff[mb] + 16 * k * 64;
+        const T* p = kbuf + koff[mb] + 16 * k * 64;
         const X8 a = join8<T>(lds_read_tr16(p), lds_read_tr16(p + 4 * 64));
         s[mb] = mma32(a, qf[k], k == 0 ? cinit : s[mb]);
       }
     }
     float mt = -INFINITY;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < NB; ++mb) {
       float mm = s[mb][0];
 #pragma unroll
       for (int e = 1; e < 16; ++e) mm = fmaxf(mm, s[mb][e]);
@@ -264,7 +292,7 @@ __global__ __launch_bounds__(win::kThreads) void attn_relpos_win_kernel(const T*
     X8 b[4], blo[4];
     float lsum = 0.f;
 #pragma unroll
-    for (int w4 = 0; w4 < 4; ++w4) {
+    for (int w4 = 0; w4 < 2 * NB; ++w4) {
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -279,31 +307,42 @@ __global__ __launch_bounds__(win::kThreads) void attn_relpos_win_kernel(const T*
       }
     }
     l_run += lsum;
-    const T* vb = vring + t * kTile;
+    const T* vbuf = kring + buf * kBuf + kTile;
 #pragma unroll
-    for (int w4 = 0; w4 < 4; ++w4) {
+    for (int w4 = 0; w4 < 2 * NB; ++w4) {
 #pragma unroll
       for (int ob = 0; ob < kMBO; ++ob) {
-        const X8 a = join8<T>(lds_read_tr16(vb + voff[w4][0] + 32 * ob), lds_read_tr16(vb + voff[w4][1] + 32 * ob));
+        const X8 a = join8<T>(lds_read_tr16(vbuf + voff[w4][0] + 32 * ob), lds_read_tr16(vbuf + voff[w4][1] + 32 * ob));
         o[ob] = mma32(a, b[w4], o[ob]);
         if (kSplitP) o[ob] = mma32(a, blo[w4], o[ob]);
       }
     }
   };
-  wait_vm<3 * 2 * kDma>();
+  // tile t is in buffer t % 3; tile 3 goes into buffer 0 once every wave is done with tile 0
+  // A wave whose 32 queries all lie past the end of the grid (the last block of the second half)
+  // skips the key loop; it still moves its share of the tiles and takes part in every barrier.
+  const bool active = q0 + wave * 32 < N;
+  using Two = std::integral_constant<int, 2>;
+  wait_vm<2 * kTDma>();  // tile 0 (tiles 1, 2 may be in flight)
   __syncthreads();
-  tile(0);
-  wait_vm<2 * 2 * kDma>();
+  if (active) tile(0, 0, Two());
+  wait_vm<kTDma>();  // tile 1 (tile 2 may be in flight)
   __syncthreads();
-  tile(1);
-  wait_vm<1 * 2 * kDma>();
+  tile_dma(3, 0);
+  if (active) tile(1, 1, Two());
+  wait_vm<kTDma>();  // tile 2 (tile 3 may be in flight)
   __syncthreads();
-  tile(2);
-  wait_vm<0>();
+  if (active) tile(2, 2, Two());
+  wait_vm<0>();  // tile 3
   __syncthreads();
-  tile(3);
+  if (active) {
+    if (4 * 3 + 2 < H)
+      tile(3, 0, Two());
+    else
+      tile(3, 0, std::integral_constant<int, 1>());
+  }
 
-  // ---- 6. normalise and store: lane holds O^T[32*ob + 8*a + 4*hh + b][query n]
+  // ---- 4. normalise and store: lane holds O^T[32*ob + 8*a + 4*hh + b][query n]
   const float inv = 1.f / sum_with_partner32(l_run);
   if (qvalid) {
     T* orow = out + u * unit_elems + qidx * kHD;
@@ -334,7 +373,7 @@ static hipError_t launch_win(const void* q, const void* kt, const void* v, const
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)bh), dim3(win::kThreads), win::kLdsBytes, stream, (const T*)q,
+  hipLaunchKernelGGL(kern, dim3((unsigned)(2 * bh)), dim3(win::kThreads), win::kLdsBytes, stream, (const T*)q,
                      (const T*)kt, (const T*)v, (const T*)table, (T*)out, h, w, scale);
   return hipGetLastError();
 }

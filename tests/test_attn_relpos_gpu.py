@@ -43,9 +43,11 @@ def run_gpu(hip, arrays, h, w, scale, dtype):
 # The reference test geometries (tests/kernels.rs:23, tests/cpu_gemm.rs:37) with its N(0,1) tables,
 # plus small and ragged shapes: a 2x3 grid with hd 8, a single grid row, and odd sizes; 64-column
 # grids with hd 80 of 1, 2, 3, 6 and 37 rows (ring shorter than its depth, odd tile counts, a partial
-# last query block).
+# last query block); window grids with hd 80 of 13..16 rows (a full or half-empty last key tile, idle
+# query blocks).
 SMALL = [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (2, 3, 2, 8), (1, 5, 2, 16), (5, 33, 2, 32),
-         (3, 40, 2, 128), (9, 17, 2, 48), (1, 64, 2, 80), (2, 64, 1, 80), (3, 64, 2, 80), (6, 64, 2, 80), (37, 64, 3, 80)]
+         (3, 40, 2, 128), (9, 17, 2, 48), (1, 64, 2, 80), (2, 64, 1, 80), (3, 64, 2, 80), (6, 64, 2, 80),
+         (37, 64, 3, 80), (16, 16, 2, 80), (13, 12, 3, 80), (15, 14, 2, 80)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
