@@ -43,7 +43,7 @@ constexpr int kMBO = 3;        // 32-row blocks of O^T (rows 80..95 are not stor
 constexpr int kTiles = 4;      // key tiles per unit
 constexpr int kRing = 3;       // tile buffers
 constexpr int kTile = kHD * 64;                  // elements of a kT tile [d][64] and of a V tile [64][80]
-constexpr int kKDma = kTile * 2 / 256 / kWaves;  // 4-byte DMAs of a kT tile per wave: 10
+constexpr int kKDma = 3;                         // 1 KB units of a kT tile per wave (12 >= 10: 2 repeats)
 constexpr int kVDma = 3;                         // 1 KB units of a V tile per wave (12 >= 10: 2 repeats)
 constexpr int kTDma = kKDma + kVDma;             // DMAs per wave per tile
 constexpr int kQRows = kWaves * 32;              // q rows of a half unit
@@ -52,7 +52,8 @@ constexpr int kTRows = 64;                       // table rows in LDS: Th at [0,
 constexpr int kTbDma = 3;                        // 1 KB units of the table per wave (12 >= 10: 2 repeats)
 constexpr int kRhsRows = 17;                     // per-wave bias scratch rows (16 + one junk row)
 constexpr float kSlack = 8.0f;
-static_assert(kTile * 2 % (256 * kWaves) == 0 && kQRows * kHD * 2 % (1024 * kWaves) == 0, "DMA split");
+static_assert(kQRows * kHD * 2 % (1024 * kWaves) == 0, "DMA split");
+static_assert(kTile * 2 <= kKDma * kWaves * 1024, "kT units");
 static_assert(kTile * 2 <= kVDma * kWaves * 1024 && kTRows * kHD * 2 <= kTbDma * kWaves * 1024, "units");
 
 // Buffer b is a kT tile at 2 b kTile and a V tile right after it; the last V tile is followed by 16
@@ -107,22 +108,25 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   const bool qvalid = qidx < N;
   const int qi = qvalid ? qidx / W : 0, qj = qvalid ? qidx % W : 0;
   const float sc = scale * kLog2e;
-  const char* kb = reinterpret_cast<const char*>(kt + u * unit_elems);
+  // kT goes through a buffer descriptor of the unit's kT: a 16-byte group may run 2 keys past the
+  // unit's end (a 14-column grid row's second group), and those dwords read 0
+  const i32x4 krsrc = buffer_rsrc(kt + u * unit_elems, (unsigned)(sizeof(T) * unit_elems));
   const char* vb = reinterpret_cast<const char*>(v + u * unit_elems);
 
   // This wave's DMAs of K/V tile t into buffer buf (kTDma of them). Slots outside the grid read key 0.
   auto tile_dma = [&](int t, int buf) {
 #pragma unroll
     for (int p = 0; p < kKDma; ++p) {
-      // kT: DMA i covers rows 2i, 2i + 1 of the tile; this lane's slot pair sits at swizzled position
-      // 2 * (lane & 31) of row d = 2i + hh (W is even, so a pair is all in or all out)
-      const int i = wave * kKDma + p;
-      const int d = 2 * i + hh;
-      const int pos = 2 * (lane & 31);
-      const int slot = (((pos >> 2) ^ kswz(d & 3)) << 2) + (pos & 3);
-      const int row = 4 * t + (slot >> 4), kap = slot & 15;
+      // kT: unit i covers rows 8i .. 8i+7 of the tile, a lane 16 bytes (8 slots) of row 8i + lane/8: the
+      // swizzle keeps 16-byte pairs of 8-byte chunks together, so they are the 8 consecutive slots
+      // from slot 4c = one grid row's columns kap .. kap+7 (kap = 0 or 8); units 10, 11 repeat 0, 1
+      const int i0 = wave + kWaves * p;
+      const int i = i0 < 10 ? i0 : i0 - 10;
+      const int d = 8 * i + (lane >> 3);
+      const int c = (2 * (lane & 7)) ^ kswz(d & 3);
+      const int row = 4 * t + (c >> 2), kap = 4 * (c & 3);
       const bool ok = kap < W && row < H;
-      dma4(kb, (unsigned)(sizeof(T) * (d * N + (ok ? row * W + kap : 0))), lds0 + (buf * kBuf + i * 128) * 2);
+      bdma16(krsrc, (unsigned)(sizeof(T) * (d * N + (ok ? row * W + kap : 0))), lds0 + (buf * kBuf + i * 512) * 2);
     }
 #pragma unroll
     for (int p = 0; p < kVDma; ++p) {

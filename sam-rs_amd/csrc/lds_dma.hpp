@@ -24,6 +24,25 @@ __device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned l
                : "memory", "m0");
 }
 
+// Raw buffer descriptor for `bytes` bytes at p (wave-uniform): buffer loads past the end read 0, range
+// checked per dword. Word 3 selects the 32-bit raw data format.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* p, unsigned bytes) {
+  const unsigned long a = (unsigned long)p;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(unsigned)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffff));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+// dma16 through a buffer descriptor: lane l's 16 bytes at byte offset off land at lds + 16 l; the
+// dwords past the descriptor's range land as 0.
+__device__ __forceinline__ void bdma16(i32x4 rsrc, unsigned off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(off), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+}
+
 // LDS byte address of a pointer into dynamic shared memory.
 __device__ __forceinline__ unsigned lds_addr(const void* p) {
   return (unsigned)(size_t)(const __attribute__((address_space(3))) char*)(p);
