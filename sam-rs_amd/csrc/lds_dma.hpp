@@ -2,9 +2,9 @@
 // explicit vector-memory waits.
 //
 // The DMAs are issued through inline asm so that the compiler inserts no waits of its own before later
-// LDS reads (it cannot tell which LDS region a DMA writes); a kernel using them issues no other vector
-// loads and waits explicitly with wait_vm, whose count relies on a wave's vector-memory operations
-// completing in issue order. M0 is written by every DMA and read by nothing else in these kernels
+// LDS reads (it cannot tell which LDS region a DMA writes). A kernel using them issues no other vector
+// memory operation while DMAs are in flight, except stores it counts itself, and waits explicitly with
+// wait_vm, whose count relies on a wave's vector-memory operations completing in issue order. M0 is written by every DMA and read by nothing else in these kernels
 // (gfx950 LDS instructions do not use it), hence the clobber of a register the compiler reserves.
 #pragma once
 #include "common.hpp"
@@ -13,12 +13,8 @@
 
 namespace samhip {
 
-// Lane l's 4 bytes at base + off land at LDS byte address lds + 4 l. base is wave-uniform (SGPRs),
+// Lane l's 16 bytes at base + off land at LDS byte address lds + 16 l. base is wave-uniform (SGPRs),
 // off this lane's byte offset from it, lds wave-uniform.
-__device__ __forceinline__ void dma4(const void* base, unsigned off, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
-}
-// The same with 16 bytes a lane (lds + 16 l).
 __device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
                : "memory", "m0");
@@ -59,13 +55,6 @@ __device__ __forceinline__ i16x4 lds_read_tr16_at(unsigned addr) {
 __device__ __forceinline__ unsigned opaque(unsigned v) {
   asm volatile("" : "+v"(v));
   return v;
-}
-
-// Makes x's current value an input and output of an empty volatile asm statement: the computation of
-// x cannot be moved past this point (a barrier is no obstacle to moving pure arithmetic otherwise).
-template <typename V>
-__device__ __forceinline__ void pin(V& x) {
-  asm volatile("" : "+v"(x));
 }
 
 // Waits until at most N of this wave's vector-memory operations are outstanding, i.e. everything
