@@ -88,8 +88,9 @@ int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, vo
  * f32 tables rope_cos / rope_sin [rope_rows, d] (table row = index % rope_rows), the other rows are
  * used as they are; n_rope_q = n_rope_k = 0 disables it (the tables may then be NULL).
  * Workspace: sam_hip_flash_attn_workspace_size() bytes of device memory (16-byte aligned), for the
- * key-split partial results and the rotated keys; it may be NULL when that size is 0. The size
- * depends on the current device's CU count: query it on the device that runs the call.
+ * key-split partial results and, when n_rope_k > 0, the rotated keys and queries; it may be NULL when
+ * that size is 0. The size depends on the current device's CU count: query it on the device that runs
+ * the call.
  * Limits: d % 8 == 0, d <= 256; scale >= 0; pointers and strides 16-byte aligned; out must not
  * overlap k, v or the workspace. f32 is rejected (SAM_HIP_EDTYPE), as by the reference's GPU flash
  * attention.

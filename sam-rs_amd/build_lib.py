@@ -25,7 +25,7 @@ SOURCES = [
     "deform_attn.hip",
     "relpos_softmax.hip",
     "qkv_split.hip",
-    "flash_attn.hip",
+    "flash_attn.hip", "flash_attn_d256.hip",
     "rope.hip",
     "sam_hip_abi.cpp",
 ]

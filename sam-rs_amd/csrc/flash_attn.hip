@@ -378,16 +378,21 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p) {
 template <typename T, int DP, int NW>
 static hipError_t launch_flash(FlashParams p, bool ropeq, hipStream_t stream) {
   typedef FlashGeom<T, DP, NW> FG;
-  auto kern = ropeq ? flash_fwd_kernel<T, DP, NW, true> : flash_fwd_kernel<T, DP, NW, false>;
-  static bool attr_set[2] = {false, false};  // one-time opt-in to more than 64 KB of dynamic LDS
-  if (!attr_set[ropeq]) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)FG::LDS);
-    if (e != hipSuccess) return e;
-    attr_set[ropeq] = true;
+  hipError_t e;
+  if (DP == 256 && flash256_eligible(p, (int)sizeof(T))) {
+    e = flash256_launch(__is_same(T, f16) ? kF16 : kBF16, p, ropeq, stream);
+  } else {
+    auto kern = ropeq ? flash_fwd_kernel<T, DP, NW, true> : flash_fwd_kernel<T, DP, NW, false>;
+    static bool attr_set[2] = {false, false};  // one-time opt-in to more than 64 KB of dynamic LDS
+    if (!attr_set[ropeq]) {
+      e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)FG::LDS);
+      if (e != hipSuccess) return e;
+      attr_set[ropeq] = true;
+    }
+    const long blocks = (long)p.b * p.h * p.qblocks * p.nsplit;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(FG::NT), FG::LDS, stream, p);
+    e = hipGetLastError();
   }
-  const long blocks = (long)p.b * p.h * p.qblocks * p.nsplit;
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(FG::NT), FG::LDS, stream, p);
-  hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nsplit == 1) return e;
   const long rows = (long)p.b * p.h * p.lq;
   hipLaunchKernelGGL((flash_combine_kernel<T, DP>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, p);

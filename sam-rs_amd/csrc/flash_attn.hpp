@@ -27,10 +27,25 @@ int flash_queries_per_block(int d);
 void flash_plan(int b, int h, int lq, int lk, int d, int cus, int* qblocks, int* nsplit, int* tps);
 size_t flash_partial_bytes(int b, int h, int lq, int d, int nsplit);
 hipError_t flash_attn_half(int dtype, FlashParams p, bool ropeq, hipStream_t stream);
+// The head-dim-256 kernel (flash_attn_d256.hip): whether it takes p, and its launch (main kernel only).
+bool flash256_eligible(const FlashParams& p, int elem_bytes);
+hipError_t flash256_launch(int dtype, FlashParams p, bool ropeq, hipStream_t stream);
 
 // x [b, l, h, d] (strides sx) -> out (strides so): row r < nrot rotated with table row r % trows,
 // the other rows copied.
 hipError_t rope_rows(int dtype, const void* x, const long* sx, void* out, const long* so, int b, int l, int h, int d,
                      const float* cos_t, const float* sin_t, int trows, int nrot, hipStream_t stream);
+// One f16 / bf16 row set of a rope_rows2 launch (total = b * l * h * d / 8 threads).
+struct RopeJob {
+  const void* x;
+  void* out;
+  long sx[3], so[3];
+  int b, l, h, nrot;
+  long total;
+};
+RopeJob rope_job(const void* x, const long* sx, void* out, const long* so, int b, int l, int h, int d, int nrot);
+// rope_rows over job a and, if b is not null, job b in one launch (f16 / bf16; both with head dim d).
+hipError_t rope_rows2(int dtype, const RopeJob& a, const RopeJob* b, int d, const float* cos_t, const float* sin_t,
+                      int trows, hipStream_t stream);
 
 }  // namespace samhip

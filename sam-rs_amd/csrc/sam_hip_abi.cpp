@@ -171,16 +171,21 @@ int device_cus() {
 
 struct FlashPlan {
   int qblocks, nsplit, tps;
-  size_t partial_bytes, rope_bytes, total;
+  size_t partial_bytes, krot_bytes, qrot_bytes, total;
 };
 
+size_t round256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Workspace: key-split partials, then (when keys are rotated) the rotated keys and room for the rotated
+// queries, both contiguous [b, l, h, d].
 FlashPlan plan_flash(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k) {
   FlashPlan pl;
   samhip::flash_plan(b, h, lq, lk, d, device_cus(), &pl.qblocks, &pl.nsplit, &pl.tps);
-  pl.partial_bytes = (samhip::flash_partial_bytes(b, h, lq, d, pl.nsplit) + 255) / 256 * 256;
+  pl.partial_bytes = round256(samhip::flash_partial_bytes(b, h, lq, d, pl.nsplit));
   const size_t elem = dtype == 0 ? 4 : 2;
-  pl.rope_bytes = n_rope_k > 0 ? (size_t)b * lk * h * d * elem : 0;
-  pl.total = pl.partial_bytes + pl.rope_bytes;
+  pl.krot_bytes = n_rope_k > 0 ? round256((size_t)b * lk * h * d * elem) : 0;
+  pl.qrot_bytes = n_rope_k > 0 ? round256((size_t)b * lq * h * d * elem) : 0;
+  pl.total = pl.partial_bytes + pl.krot_bytes + pl.qrot_bytes;
   return pl;
 }
 
@@ -242,15 +247,26 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
   p.k = k;
   p.v = v;
   p.out = out;
+  bool ropeq = n_rope_q > 0;
   if (n_rope_k > 0) {
-    // keys rotated into the workspace as a contiguous [b, lk, h, d] copy
+    // keys, and the queries when they are rotated too, go into the workspace as contiguous [b, l, h, d]
+    // copies, in one launch; the attention kernel then reads plain operands
     void* kr = ws + pl.partial_bytes;
-    long sr[3];
-    contiguous_strides(sr, lk, h, d);
-    hipError_t e = samhip::rope_rows(dtype, k, p.sk, kr, sr, b, lk, h, d, rope_cos, rope_sin, rope_rows, n_rope_k, s);
-    if (e != hipSuccess) return check_launch(e, "flash-attn (key rotation)");
+    void* qr = ws + pl.partial_bytes + pl.krot_bytes;
+    long skr[3], sqr[3];
+    contiguous_strides(skr, lk, h, d);
+    contiguous_strides(sqr, lq, h, d);
+    const samhip::RopeJob jk = samhip::rope_job(k, p.sk, kr, skr, b, lk, h, d, n_rope_k);
+    const samhip::RopeJob jq = samhip::rope_job(q, p.sq, qr, sqr, b, lq, h, d, n_rope_q);
+    hipError_t e = samhip::rope_rows2(dtype, jk, ropeq ? &jq : nullptr, d, rope_cos, rope_sin, rope_rows, s);
+    if (e != hipSuccess) return check_launch(e, "flash-attn (rotation)");
     p.k = kr;
-    for (int i = 0; i < 3; ++i) p.sk[i] = sr[i];
+    for (int i = 0; i < 3; ++i) p.sk[i] = skr[i];
+    if (ropeq) {
+      p.q = qr;
+      for (int i = 0; i < 3; ++i) p.sq[i] = sqr[i];
+      ropeq = false;
+    }
   }
   p.b = b;
   p.h = h;
@@ -268,8 +284,8 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
   p.rcos = rope_cos;
   p.rsin = rope_sin;
   p.rrows = rope_rows;
-  p.nrq = n_rope_q;
-  return check_launch(samhip::flash_attn_half(dtype, p, n_rope_q > 0, s), "flash-attn");
+  p.nrq = ropeq ? n_rope_q : 0;
+  return check_launch(samhip::flash_attn_half(dtype, p, ropeq, s), "flash-attn");
 }
 
 int sam_hip_rope(const void* x, const float* cos_t, const float* sin_t, void* out, int dtype, int b, int l, int h,

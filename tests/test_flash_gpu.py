@@ -34,7 +34,8 @@ def rounded(r, shape, dtype, std=1.0):
 # head dims of the reference's callers (Hiera 96 at its widest stage, SAM 3 ViT 64, memory attention
 # 256), and shapes whose few query blocks force the key-split path.
 BLHD = [(1, 5, 7, 2, 16), (2, 33, 65, 3, 64), (1, 40, 100, 1, 256), (2, 130, 200, 4, 96), (1, 64, 64, 8, 64),
-        (1, 300, 1000, 2, 128), (1, 1, 1, 1, 8), (1, 17, 3000, 1, 64), (3, 49, 49, 2, 32), (1, 257, 129, 1, 256)]
+        (1, 300, 1000, 2, 128), (1, 1, 1, 1, 8), (1, 17, 3000, 1, 64), (3, 49, 49, 2, 32), (1, 257, 129, 1, 256),
+        (2, 130, 517, 3, 256), (1, 70, 33, 2, 256), (1, 128, 64, 1, 256)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
@@ -70,6 +71,34 @@ def test_strided_views_are_read_in_place(hip):
     ref = hip.flash_attn(q.contiguous(), k.contiguous(), v.contiguous())
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
+
+
+def test_strided_views_d256(hip):
+    """Head dim 256 read in place from a packed [B, L, 3, H, D] projection (row stride 6 x 256)."""
+    r = np.random.default_rng(4)
+    b, l, h, d = 1, 150, 2, 256
+    packed = to_dev(rounded(r, (b, l, 3, h, d), "bf16"), "bf16")
+    q, k, v = packed[:, :, 0], packed[:, :, 1], packed[:, :, 2]
+    got = hip.flash_attn(q, k, v)
+    ref = hip.flash_attn(q.contiguous(), k.contiguous(), v.contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_flash_d256_growing_scores(hip, dtype):
+    """Key norms growing along the sequence (0.03 to 10) push each query's running max past the lazy
+    rescale's slack 2 to 4 times, mid-loop: b x h = 256 query blocks leave the keys unsplit, so every
+    workgroup walks all 10 key tiles and rescales its accumulated O on the way."""
+    r = np.random.default_rng(77)
+    b, h, lq, lk, d = 2, 128, 32, 640, 256
+    q = rounded(r, (b, lq, h, d), dtype)
+    grow = (np.linspace(0.1, 10.0, lk, dtype=np.float32) ** 1.5 / np.float32(10.0 ** 0.5))[None, :, None, None]
+    k = oracle.round_to((r.standard_normal((b, lk, h, d)).astype(np.float32) * grow), dtype)
+    v = rounded(r, (b, lk, h, d), dtype)
+    got = hip.flash_attn(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype))
+    torch.cuda.synchronize()
+    check(got.float().cpu().numpy(), oracle.mha_blhd(q, k, v), dtype, f"flash_attn growing scores {dtype}")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
@@ -129,6 +158,27 @@ def test_rope_attention_small(hip, side, frames, n_ptr, dtype):
     if dtype == "f16":
         want32 = oracle.rope_attention(q, k, v, cos, sin, n_ptr)
         check(got[0].float().cpu().numpy(), want32, dtype, "rope_attention vs f32 rotation")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("d,lq,n_rope_q", [(256, 200, 150), (64, 130, 130)])
+def test_rope_on_queries_only(hip, d, lq, n_rope_q, dtype):
+    """Queries rotated and keys not (n_rope_k = 0): the rotation then happens while the attention kernel
+    loads Q, with the same rounding as the separate pass (f32 products and sum, one rounding)."""
+    side, lk = 8, 300
+    cos, sin = oracle.rope_tables(side, 1.0, d, 10000.0)
+    r = np.random.default_rng(31 + d)
+    q, k, v = (rounded(r, (1, n, 1, d), dtype) for n in (lq, lk, lk))
+    got = hip._flash(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype), torch.empty(1, lq, 1, d, device="cuda",
+                     dtype=TORCH_DT[dtype]), "blhd", d ** -0.5, torch.from_numpy(cos).cuda(),
+                     torch.from_numpy(sin).cuda(), n_rope_q=n_rope_q, n_rope_k=0)
+    torch.cuda.synchronize()
+    qr = q[0, :, 0].copy()
+    for i in range(0, n_rope_q, len(cos)):
+        j = min(n_rope_q, i + len(cos))
+        qr[i:j] = oracle.round_to(oracle.rope(q[0, i:j, 0], cos[:j - i], sin[:j - i]), dtype)
+    want = oracle.sdpa(qr[None, None], k[0, :, 0][None, None], v[0, :, 0][None, None])[0, 0]
+    check(got[0, :, 0].float().cpu().numpy(), want, dtype, f"rope on queries only d{d} {dtype}")
 
 
 @pytest.mark.parametrize("case", ["self", "cross"])
