@@ -2,10 +2,14 @@
 // explicit vector-memory waits.
 //
 // The DMAs are issued through inline asm so that the compiler inserts no waits of its own before later
-// LDS reads (it cannot tell which LDS region a DMA writes). A kernel using them issues no other vector
-// memory operation while DMAs are in flight, except stores it counts itself, and waits explicitly with
-// wait_vm, whose count relies on a wave's vector-memory operations completing in issue order. M0 is written by every DMA and read by nothing else in these kernels
-// (gfx950 LDS instructions do not use it), hence the clobber of a register the compiler reserves.
+// LDS reads (it cannot tell which LDS region a DMA writes). Kernels wait for them explicitly with
+// wait_vm. A wave's vector-memory operations complete in issue order, so wait_vm<N> is correct when N
+// counts operations issued after the awaited one; other vector-memory operations in between only make
+// the wait longer. The compiler's own waits for its loads count only its own operations, so a load
+// issued before DMAs is waited for together with them: kernels load what the compiler tracks before
+// the DMAs that should stay in flight past its use, or wait for it in a compiler-visible s_waitcnt.
+// M0 is written by every DMA and read by nothing else in these kernels (gfx950 LDS instructions do
+// not use it), hence the clobber of a register the compiler reserves.
 #pragma once
 #include "common.hpp"
 
