@@ -112,7 +112,8 @@ def traffic_from_profiles():
 
 
 class Timer:
-    """HIP events recorded on the launch stream around each call; the average launch time in ms."""
+    """One pair of HIP events on the launch stream around reps back-to-back calls; the average call
+    time in ms (no markers between the calls)."""
 
     def __init__(self, torch, stream):
         self.torch, self.stream = torch, stream
@@ -120,14 +121,14 @@ class Timer:
     def avg_ms(self, fn, reps, warmup=2):
         for _ in range(warmup):
             fn()
-        ev = [(self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True))
-              for _ in range(reps)]
-        for a, b in ev:
-            a.record(self.stream)
-            fn()
-            b.record(self.stream)
         self.torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in ev) / reps
+        a, b = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
+        a.record(self.stream)
+        for _ in range(reps):
+            fn()
+        b.record(self.stream)
+        self.torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
 
 
 def check(lib, rc):
@@ -317,15 +318,22 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # The timed region: plain steps, bracketed by events on the launch stream. Events between the layers
+    # would put host calls and queue markers between the kernels and lengthen the step by about a
+    # quarter, so the per-kernel durations come from a second region right after it.
     t0e, t1e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    evs = ([], [], [], [])
     t0e.record(stream)
     for _ in range(args.steps):
-        step(evs)
+        step()
     t1e.record(stream)
     torch.cuda.synchronize()
     ms_total = t0e.elapsed_time(t1e)
     ms_step = ms_total / args.steps
+    # Per-kernel durations: the same steps again, each launch between its own pair of events.
+    evs = ([], [], [], [])
+    for _ in range(args.steps):
+        step(evs)
+    torch.cuda.synchronize()
     glob_ms = sum(a.elapsed_time(b) for a, b in zip(evs[0], evs[1])) / max(len(evs[0]), 1)
     win_ms = sum(a.elapsed_time(b) for a, b in zip(evs[2], evs[3])) / max(len(evs[2]), 1)
     if args.layers != "all":
