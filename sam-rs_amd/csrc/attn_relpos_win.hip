@@ -50,7 +50,7 @@ constexpr int kQRows = kWaves * 32;              // q rows of a half unit
 constexpr int kQDma = kQRows * kHD * 2 / 1024 / kWaves;  // 1 KB units of q per wave: 5
 constexpr int kTRows = 64;                       // table rows in LDS: Th at [0, 32), Tw at [32, 64)
 constexpr int kTbDma = 3;                        // 1 KB units of the table per wave (12 >= 10: 2 repeats)
-constexpr int kRhsRows = 17;                     // per-wave bias scratch rows (16 + one junk row)
+constexpr int kRhsRows = 18;                     // per-wave bias scratch rows: -1 (junk), 0..15, 16 (junk)
 constexpr float kSlack = 8.0f;
 static_assert(kQRows * kHD * 2 % (1024 * kWaves) == 0, "DMA split");
 static_assert(kTile * 2 <= kKDma * kWaves * 1024, "kT units");
@@ -216,28 +216,36 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
       gh = mma32(ah, qf[s], gh);
       gw = mma32(aw, qf[s], gw);
     }
+    // Scatter along the diagonal band: accumulator element e of this lane is table row rr = re + 4 hh
+    // (re = 8 (e >> 2) + (e & 3)), which belongs to key column (row) b - rr with b = qj + W - 1
+    // (qi + H - 1). The column is clamped into [-1, 16] and scratch row c + 1 takes it: the valid
+    // columns 0..W-1 keep their row, a table row past 2W - 2 always lands on column -1, and columns
+    // W..15 and 16 are never read as valid. So each element costs a subtract, a clamp and an address.
+    float* rb = rhs + 32 + n;  // scratch row 0 = column -1
     // Rw: a lane's key columns are e = 0..15 in every 32-key block, so cinit[e] = Rw[e] / sc
+    {
+      const int b = qj + W - 1 - 4 * hh;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int rr = 8 * (e >> 2) + 4 * hh + (e & 3);
-      const int kw = qj + W - 1 - rr;
-      const bool ok = rr < 2 * W - 1 && kw >= 0 && kw < W;
-      rhs[(ok ? kw : 16) * 32 + n] = gw[e] * kLog2e;
+      for (int e = 0; e < 16; ++e) {
+        const int c = min(max(b - (8 * (e >> 2) + (e & 3)), -1), 16);
+        rb[c * 32] = gw[e] * kLog2e;
+      }
     }
     wave_sync();
     const float inv_sc = 1.f / sc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const float x = rhs[e * 32 + n];
+      const float x = rb[e * 32];
       cinit[e] = e < W ? x * inv_sc : -INFINITY;
     }
     wave_sync();
+    {
+      const int b = qi + H - 1 - 4 * hh;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int rr = 8 * (e >> 2) + 4 * hh + (e & 3);
-      const int kh = qi + H - 1 - rr;
-      const bool ok = rr < 2 * H - 1 && kh >= 0 && kh < H;
-      rhs[(ok ? kh : 16) * 32 + n] = gh[e] * kLog2e;
+      for (int e = 0; e < 16; ++e) {
+        const int c = min(max(b - (8 * (e >> 2) + (e & 3)), -1), 16);
+        rb[c * 32] = gh[e] * kLog2e;
+      }
     }
     wave_sync();
 #pragma unroll
@@ -245,7 +253,7 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
         const int row = 4 * t + 2 * mb + hh;  // < 16
-        const float x = rhs[row * 32 + n];
+        const float x = rb[row * 32];
         rh[t][mb] = row < H ? x : -INFINITY;
       }
   }
@@ -393,3 +401,4 @@ bool attn_relpos_window(int dtype, const void* q, const void* kt, const void* v,
 }
 
 }  // namespace samhip
+

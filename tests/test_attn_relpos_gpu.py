@@ -91,6 +91,45 @@ def test_vit_h_window_layer(hip, dtype):
     check(got, want, dtype, f"vit-h window {dtype}")
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("bh", [257, 768, 1024, 1600])
+def test_window_kernel_many_units(hip, bh, dtype):
+    """More half units than the 2 x CUs workgroups of the windowed kernel, so workgroups run several
+    in turn through their LDS ring: 257 units (only a few workgroups take a second half unit), 768
+    (three each), 1024 (four), 1600 (ViT-H batch 4: six or seven). The GPU runs every unit; the oracle
+    checks the first and last units, those around each multiple of 256 and a spread in between."""
+    h = w = 14
+    hd = 80
+    print(f"window many units {dtype} bh={bh}", flush=True)
+    arrays = make_inputs(h, w, bh, hd, 50 + bh, dtype)
+    scale = hd ** -0.5
+    got = run_gpu(hip, arrays, h, w, scale, dtype)
+    units = set(np.linspace(0, bh - 1, 16).astype(int).tolist())
+    for m in range(0, bh + 1, 256):
+        units.update(u for u in (m - 1, m, m + 1) if 0 <= u < bh)
+    units = sorted(units)
+    q, kt, v, table = arrays
+    want = oracle.attention_relpos(q[units], kt[units], v[units], table, h, w, scale)
+    check(got[units], want, dtype, f"window kernel bh={bh} {dtype}")
+
+
+def test_window_kernel_units_are_independent(hip):
+    """At 1600 units the windowed kernel's workgroups run several half units each: permuting the units
+    moves them to other workgroups and pipeline positions, and the output rows move with them exactly."""
+    h = w = 14
+    bh, hd = 1600, 80
+    g = torch.Generator(device="cuda").manual_seed(13)
+    q = torch.randn(bh, h * w, hd, device="cuda", generator=g).half()
+    kt = torch.randn(bh, hd, h * w, device="cuda", generator=g).half()
+    v = torch.randn(bh, h * w, hd, device="cuda", generator=g).half()
+    table = (0.02 * torch.randn(2 * h - 1 + 2 * w - 1, hd, device="cuda", generator=g)).half()
+    perm = torch.randperm(bh, device="cuda", generator=g)
+    a = hip.attention_relpos(q, kt, v, table, h, w, hd ** -0.5)
+    b = hip.attention_relpos(q[perm].contiguous(), kt[perm].contiguous(), v[perm].contiguous(), table, h, w,
+                             hd ** -0.5)
+    assert torch.equal(a[perm], b)
+
+
 def test_vit_b_f32_layers(hip):
     """ViT-B f32: windowed layer (300 x 14x14, hd 64, (27,64) tables) and global layer (12 x 64x64,
     (127,64) tables) at scale 64^-0.5; q/k/v ~ N(0, 0.3) as the qkv projection of N(0,1) tokens
