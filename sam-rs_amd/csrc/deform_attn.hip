@@ -10,10 +10,16 @@
 // weights 32 times per (q, h). Here a group of LP lanes owns one (b, q, h) pair and each lane a vector
 // of VEC consecutive d (16 bytes: 4 f32 or 8 f16/bf16), so one load per corner is a 16-byte gather and
 // a pair's corner row (D elements, contiguous in `value`) is read by its lanes in one coalesced access.
-// The L*P points of a pair are turned once into 4 (element offset, weight) corners in LDS by the
-// pair's own lanes, then every lane walks them, accumulating in f32 in the reference's (l, p, corner)
-// order. Work is bound by the gathers (64 corner rows per pair), which hit L2 / the Infinity cache:
-// `value` is read once from HBM.
+// The L*P points of a pair are turned once into 4 (offset, weight) corners in LDS by the pair's own
+// lanes, then every lane walks them, accumulating in f32 in the reference's (l, p, corner) order.
+//
+// Work is bound by the gathers (64 corner rows per pair for DINO), so two choices decide the speed:
+// - deform_attn_gather_kernel (D a multiple of VEC): branch-free corner walk through a buffer
+//   descriptor, so each wave keeps many gathers in flight, and a head-major work order in contiguous
+//   ranges per XCD, so that each XCD's 4 MB L2 holds the value rows of one or two heads (value is
+//   [B, S, H, D]: a head's row of a pixel is its own D-element run, shared with no other head).
+// - deform_attn_kernel (other D, or more than 3.75 GB of value): the same contract with scalar lanes
+//   and a branch per corner.
 #include "common.hpp"
 
 namespace samhip {
@@ -115,6 +121,102 @@ __global__ __launch_bounds__(kDeformThreads) void deform_attn_kernel(const T* __
   }
 }
 
+// The same contract through buffer-descriptor loads, for VEC-wide lanes: a skipped corner (outside
+// its level) points past the end of the descriptor, where the load returns 0, so the corner walk has
+// no branches and a wave keeps kDeformUnroll independent gathers in flight. The corner table of a pair
+// is padded to a multiple of kDeformUnroll entries with skipped corners of weight 0. One descriptor
+// covers all of `value` (wave-uniform), whose size in bytes must stay below kDeformSkip (checked by the
+// launcher).
+constexpr int kDeformUnroll = 16;
+constexpr unsigned kDeformSkip = 0xF0000000u;
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(kDeformThreads) void deform_attn_gather_kernel(const T* __restrict__ value,
+                                                                           const T* __restrict__ loc,
+                                                                           const T* __restrict__ attn,
+                                                                           T* __restrict__ out, int B, int S,
+                                                                           int Q, int H, int D, int L, int P,
+                                                                           int lp_shift, int ntab, Levels lv) {
+  typedef typename VecLoad<T, VEC>::type VT;
+  static_assert(sizeof(VT) == 16, "16-byte lanes");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int LP = 1 << lp_shift;            // lanes per (b, q, h) pair
+  const int ppw = 64 >> lp_shift;          // pairs per wave
+  const int npt = L * P;                   // points per pair
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane >> lp_shift, li = lane & (LP - 1);
+  // Work items in head-major order (h, b, q), in contiguous ranges per XCD: workgroup i runs on XCD
+  // i % 8, so an XCD's L2 holds the value rows of one or two heads instead of all of them.
+  const int nblk = gridDim.x, xcd = blockIdx.x & 7, per = nblk >> 3, rem = nblk & 7;
+  const long lin = (long)xcd * per + (xcd < rem ? xcd : rem) + (blockIdx.x >> 3);
+  const long item = (lin * (kDeformThreads / 64) + wave) * ppw + sub;
+  const long BQ = (long)B * Q;
+  const bool valid = item < BQ * H;
+  const int h = valid ? (int)(item / BQ) : 0;
+  const long bq = valid ? item % BQ : 0;  // b * Q + q
+  const long b = bq / Q;
+  const long pair = bq * H + h;  // index of the (b, q, h) pair in loc and attn
+  // corner table of this pair: ntab entries of (byte offset into value, weight)
+  int2* corners = reinterpret_cast<int2*>(smem) + ((long)wave * ppw + sub) * ntab;
+  for (int j = li; j < (ntab >> 2); j += LP) {
+    int2 c4[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) c4[c] = make_int2((int)kDeformSkip, 0);
+    if (valid && j < npt) {
+      const int l = j / P;
+      const long base = pair * npt + j;  // ((b*Q + q)*H + h)*L*P + l*P + p
+      const float wgt = to_f32(attn[base]);
+      const int Hl = lv.h[l], Wl = lv.w[l];
+      const float x = to_f32(loc[base * 2]) * (float)Wl - 0.5f;
+      const float y = to_f32(loc[base * 2 + 1]) * (float)Hl - 0.5f;
+      const float xf = floorf(x), yf = floorf(y);
+      const int x0 = (int)xf, y0 = (int)yf;
+      const float fx = x - xf, fy = y - yf;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int xx = x0 + (c & 1), yy = y0 + (c >> 1);
+        const bool in = xx >= 0 && xx < Wl && yy >= 0 && yy < Hl;
+        const float wt = wgt * ((c & 1) ? fx : 1.f - fx) * ((c >> 1) ? fy : 1.f - fy);
+        const unsigned off = (unsigned)(((b * S + lv.start[l] + (long)yy * Wl + xx) * H + h) * D * (long)sizeof(T));
+        if (in) c4[c] = make_int2((int)off, __float_as_int(wt));
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) corners[j * 4 + c] = c4[c];
+  }
+  __syncthreads();
+  if (!valid) return;
+
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)value, (short)0, (int)(unsigned)((long)B * S * H * D * (long)sizeof(T)), 0x00020000);
+  T* orow = out + bq * (long)H * D + (long)h * D;
+  for (int d0 = li * VEC; d0 < D; d0 += LP * VEC) {
+    float acc[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
+    const unsigned dbytes = (unsigned)(d0 * sizeof(T));
+    for (int j0 = 0; j0 < ntab; j0 += kDeformUnroll) {
+      int2 cw[kDeformUnroll];
+      VT vv[kDeformUnroll];
+#pragma unroll
+      for (int u = 0; u < kDeformUnroll; ++u) cw[u] = corners[j0 + u];
+#pragma unroll
+      for (int u = 0; u < kDeformUnroll; ++u)
+        vv[u] = __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((unsigned)cw[u].x + dbytes), 0, 0));
+#pragma unroll
+      for (int u = 0; u < kDeformUnroll; ++u) {
+        const float wt = __int_as_float(cw[u].y);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[i] = fmaf(wt, to_f32(vv[u][i]), acc[i]);
+      }
+    }
+    VT o;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) o[i] = from_f32<T>(acc[i]);
+    *reinterpret_cast<VT*>(orow + d0) = o;
+  }
+}
+
 template <typename T, int VEC>
 static hipError_t launch_deform(const void* value, const void* loc, const void* attn, void* out, int b, int s, int q,
                                 int h, int d, int l, int p, const Levels& lv, hipStream_t stream) {
@@ -133,8 +235,29 @@ static hipError_t launch_deform(const void* value, const void* loc, const void* 
 }
 
 template <typename T, int VEC>
+static hipError_t launch_gather(const void* value, const void* loc, const void* attn, void* out, int b, int s, int q,
+                                int h, int d, int l, int p, const Levels& lv, hipStream_t stream) {
+  const int lanes = d / VEC;
+  int shift = 3;
+  while ((1 << shift) < lanes && shift < 6) ++shift;
+  const int ppw = 64 >> shift;
+  const int ntab = (l * p * 4 + kDeformUnroll - 1) / kDeformUnroll * kDeformUnroll;
+  const long pairs = (long)b * q * h;
+  const long waves = (pairs + ppw - 1) / ppw;
+  const long blocks = (waves + kDeformThreads / 64 - 1) / (kDeformThreads / 64);
+  const size_t lds = (size_t)(kDeformThreads / 64) * ppw * ntab * sizeof(int2);
+  hipLaunchKernelGGL((deform_attn_gather_kernel<T, VEC>), dim3((unsigned)blocks), dim3(kDeformThreads), lds, stream,
+                     (const T*)value, (const T*)loc, (const T*)attn, (T*)out, b, s, q, h, d, l, p, shift, ntab, lv);
+  return hipGetLastError();
+}
+
+template <typename T, int VEC>
 static hipError_t pick_deform(const void* value, const void* loc, const void* attn, void* out, int b, int s, int q,
                               int h, int d, int l, int p, const Levels& lv, hipStream_t stream) {
+  // byte offsets into value, plus a row, stay below the skip marker
+  const long block_bytes = ((long)b * s * h * d + d) * (long)sizeof(T);
+  if (d % VEC == 0 && block_bytes < (long)kDeformSkip)
+    return launch_gather<T, VEC>(value, loc, attn, out, b, s, q, h, d, l, p, lv, stream);
   if (d % VEC == 0) return launch_deform<T, VEC>(value, loc, attn, out, b, s, q, h, d, l, p, lv, stream);
   return launch_deform<T, 1>(value, loc, attn, out, b, s, q, h, d, l, p, lv, stream);
 }

@@ -1,8 +1,9 @@
 """Parity of the multi-scale deformable attention (libsam_hip.so) with the CPU oracle, on an MI355X.
 
 Cases: the reference's own test shapes (tests/kernels.rs:65-83, tests/dino.rs:46-63) with sampling
-locations spread beyond [0, 1] so the zero padding is exercised, plus the Grounding DINO-tiny encoder and
-decoder layers at full size. Bars: f32 max-abs 1e-4 (the reference test's, tests/kernels.rs:78); f16
+locations spread beyond [0, 1] so the zero padding is exercised, shapes that take each of the two
+kernels (16-byte lanes when D allows, scalar lanes otherwise) and multi-batch grids of hundreds of
+workgroups, plus the Grounding DINO-tiny encoder and decoder layers at full size. Bars: f32 max-abs 1e-4 (the reference test's, tests/kernels.rs:78); f16
 and bf16 max-abs against the f32 oracle on the same rounded inputs: 2e-3 (f16) and the reference
 test's 5e-2 (bf16, whose 8-bit inputs and output cannot do better on values ~N(0,1)).
 """
@@ -53,6 +54,9 @@ CASES = [
     ("batch2-odd-d", [(6, 5), (3, 3)], 2, 11, 3, 20, 2, 0.7),
     ("single-level", [(16, 16)], 1, 64, 2, 64, 8, 0.4),
     ("d-not-multiple-of-4", [(5, 7), (2, 4)], 1, 9, 2, 6, 3, 0.5),
+    # hundreds of workgroups: the head-major, per-XCD work order crosses head and batch boundaries
+    ("batch2-many-blocks", [(30, 40), (15, 20), (8, 10), (4, 5)], 2, 3001, 8, 32, 4, 0.6),
+    ("five-heads-d16", [(12, 10), (6, 5)], 1, 777, 5, 16, 3, 0.5),
 ]
 
 
