@@ -106,40 +106,53 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   const int q0 = (blk & 1) * kQRows;  // first query of this half unit
   const int qidx = q0 + wave * 32 + n;
   const bool qvalid = qidx < N;
-  const int qi = qvalid ? qidx / W : 0, qj = qvalid ? qidx % W : 0;
+  // qidx < 256 and W <= 16: (qidx + 0.5) / W lies at least 0.5 / W from an integer, far beyond the
+  // error of the approximate reciprocal and product, so truncation gives the exact quotient
+  const int qdiv = (int)(((float)qidx + 0.5f) * __builtin_amdgcn_rcpf((float)W));
+  const int qi = qvalid ? qdiv : 0, qj = qvalid ? qidx - qdiv * W : 0;
   const float sc = scale * kLog2e;
-  // kT goes through a buffer descriptor of the unit's kT: a 16-byte group may run 2 keys past the
-  // unit's end (a 14-column grid row's second group), and those dwords read 0
+  // kT and V go through buffer descriptors of the unit's kT and V, so a lane's DMA offset is the same
+  // for every tile (the tile's start is a wave-uniform soffset): slots past a grid row's W columns and
+  // rows past H read other keys of the unit (their bias is -inf, so P = 0) or, past the unit's end, 0
   const i32x4 krsrc = buffer_rsrc(kt + u * unit_elems, (unsigned)(sizeof(T) * unit_elems));
-  const char* vb = reinterpret_cast<const char*>(v + u * unit_elems);
+  const i32x4 vrsrc = buffer_rsrc(v + u * unit_elems, (unsigned)(sizeof(T) * unit_elems));
+  unsigned kdof[kKDma], vdof[kVDma];
+#pragma unroll
+  for (int p = 0; p < kKDma; ++p) {
+    // kT: unit i covers rows 8i .. 8i+7 of the tile, a lane 16 bytes (8 slots) of row 8i + lane/8: the
+    // swizzle keeps 16-byte pairs of 8-byte chunks together, so they are the 8 consecutive slots
+    // from slot 4c = one grid row's columns kap .. kap+7 (kap = 0 or 8); units 10, 11 repeat 0, 1
+    const int i0 = wave + kWaves * p;
+    const int i = i0 < 10 ? i0 : i0 - 10;
+    const int d = 8 * i + (lane >> 3);
+    const int c = (2 * (lane & 7)) ^ kswz(d & 3);
+    kdof[p] = (unsigned)(sizeof(T) * (d * N + (c >> 2) * W + 4 * (c & 3)));
+  }
+#pragma unroll
+  for (int p = 0; p < kVDma; ++p) {
+    // V: unit j covers elements [512 j, 512 j + 512) of the [64 slots][80] tile, a lane 8 columns of
+    // one slot; units 10 and 11 repeat units 0 and 1
+    const int j0 = wave + kWaves * p;
+    const int j = j0 < 10 ? j0 : j0 - 10;
+    const int e = j * 512 + 8 * lane;
+    const int slot = e / kHD, col = e % kHD;
+    vdof[p] = (unsigned)(sizeof(T) * (((slot >> 4) * W + (slot & 15)) * kHD + col));
+  }
 
-  // This wave's DMAs of K/V tile t into buffer buf (kTDma of them). Slots outside the grid read key 0.
+  // This wave's DMAs of K/V tile t (grid rows 4t .. 4t+3) into buffer buf (kTDma of them)
   auto tile_dma = [&](int t, int buf) {
+    const unsigned kso = (unsigned)(sizeof(T) * 4 * t * W), vso = kso * kHD;
 #pragma unroll
     for (int p = 0; p < kKDma; ++p) {
-      // kT: unit i covers rows 8i .. 8i+7 of the tile, a lane 16 bytes (8 slots) of row 8i + lane/8: the
-      // swizzle keeps 16-byte pairs of 8-byte chunks together, so they are the 8 consecutive slots
-      // from slot 4c = one grid row's columns kap .. kap+7 (kap = 0 or 8); units 10, 11 repeat 0, 1
       const int i0 = wave + kWaves * p;
       const int i = i0 < 10 ? i0 : i0 - 10;
-      const int d = 8 * i + (lane >> 3);
-      const int c = (2 * (lane & 7)) ^ kswz(d & 3);
-      const int row = 4 * t + (c >> 2), kap = 4 * (c & 3);
-      const bool ok = kap < W && row < H;
-      bdma16(krsrc, (unsigned)(sizeof(T) * (d * N + (ok ? row * W + kap : 0))), lds0 + (buf * kBuf + i * 512) * 2);
+      bdma16s(krsrc, kdof[p], kso, lds0 + (buf * kBuf + i * 512) * 2);
     }
 #pragma unroll
     for (int p = 0; p < kVDma; ++p) {
-      // V: unit j covers elements [512 j, 512 j + 512) of the [64 slots][80] tile, a lane 8 columns of
-      // one slot; units 10 and 11 repeat units 0 and 1
       const int j0 = wave + kWaves * p;
       const int j = j0 < 10 ? j0 : j0 - 10;
-      const int e = j * 512 + 8 * lane;
-      const int slot = e / kHD, col = e % kHD;
-      const int row = 4 * t + (slot >> 4), kap = slot & 15;
-      const bool ok = kap < W && row < H;
-      dma16(vb, (unsigned)(sizeof(T) * ((ok ? (row * W + kap) * kHD : 0) + col)),
-            lds0 + (buf * kBuf + kTile + j * 512) * 2);
+      bdma16s(vrsrc, vdof[p], vso, lds0 + (buf * kBuf + kTile + j * 512) * 2);
     }
   };
 

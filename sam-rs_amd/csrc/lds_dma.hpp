@@ -43,6 +43,12 @@ __device__ __forceinline__ void bdma16(i32x4 rsrc, unsigned off, unsigned lds) {
                : "memory", "m0");
 }
 
+// bdma16 with a wave-uniform byte offset soff added to every lane's offset (buffer soffset).
+__device__ __forceinline__ void bdma16s(i32x4 rsrc, unsigned off, unsigned soff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(off), "s"(rsrc), "s"(soff), "s"(lds)
+               : "memory", "m0");
+}
+
 // LDS byte address of a pointer into dynamic shared memory.
 __device__ __forceinline__ unsigned lds_addr(const void* p) {
   return (unsigned)(size_t)(const __attribute__((address_space(3))) char*)(p);
