@@ -225,6 +225,31 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
 
+    # SAM image preprocessing (image_proc::prepare): a u8 RGB image resized so its longest side is 1024,
+    # normalised and zero padded into [1, 3, 1024, 1024], for a 1920x1080 frame and a 4000x3000 photo.
+    for name, (ih, iw) in (("1080p", (1080, 1920)), ("12mp", (3000, 4000))):
+        img = torch.randint(0, 256, (ih, iw, 3), dtype=torch.uint8, device=dev, generator=g)
+        nh, nw, _ = sam_hip.resized_hw(ih, iw, 1024)
+        for dname, odt in (("f16", torch.float16), ("f32", torch.float32)):
+            out = torch.empty((1, 3, 1024, 1024), dtype=odt, device=dev)
+            mean = (ctypes.c_float * 3)(*sam_hip.SAM_MEAN)
+            std = (ctypes.c_float * 3)(*sam_hip.SAM_STD)
+            code = CODE[dname]
+
+            def run():
+                check(lib, lib.sam_hip_preprocess(img.data_ptr(), out.data_ptr(), code, ih, iw, nh, nw, 1024, mean,
+                                                  std, sp))
+
+            ms = timer.avg_ms(run, 50)
+            nbytes = float(ih * iw * 3 + 3 * 1024 * 1024 * out.element_size())
+            res[f"preprocess_{name}_{dname}"] = {
+                "workload": f"SAM image preprocessing: u8 {iw}x{ih} RGB -> resize to {nw}x{nh} (antialiased), "
+                            f"normalise, pad to 3x1024x1024 {dname}",
+                "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
+                "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            }
+
     # SAM ViT-B encoder attention layers, f32 (12 heads x 64): window 300 x 14x14, global 12 x 64x64.
     for name, bh, hw in (("window", 300, 14), ("global", 12, 64)):
         n = hw * hw

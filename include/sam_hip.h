@@ -76,6 +76,20 @@ int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, vo
                         int q, int h, int d, int l, int p, const int* shapes, void* stream);
 
 /*
+ * SAM image preprocessing: antialiased triangle-filter resize (PIL's bilinear) of an RGB u8 image
+ * img [h, w, 3] to nh x nw, then (x - mean[c]) / std_dev[c], zero padded at the bottom and right into
+ * out [3, size, size] of `dtype`. mean and std_dev are host arrays of 3 floats.
+ * Replaces kernels::preprocess (kernels.rs:1063-1070; cuda::Preprocess, kernels.rs:1396-1430;
+ * sam.cu:162-204), the GPU side of image_proc::prepare / prepare_square (image_proc.rs:21-53), with
+ * the arithmetic of their CPU side image_proc::resize_normalize (image_proc.rs:57-96): f32 output
+ * equals it bit for bit, f16 / bf16 output is that value rounded to nearest even.
+ * Limits: 1 <= nh, nw <= size; std_dev[c] != 0; at most 64 filter taps per output pixel and axis
+ * (w / nw and h / nh at most 31); fewer than 2^31 input and output elements.
+ */
+int sam_hip_preprocess(const void* img, void* out, int dtype, int h, int w, int nh, int nw, int size,
+                       const float* mean, const float* std_dev, void* stream);
+
+/*
  * Flash attention without a mask, f16 / bf16, on [b, l, h, d] operands given by (batch, row, head)
  * element strides (NULL = contiguous [b, l, h, d]; the head dimension is always contiguous):
  *   out[b, i, h, :] = softmax_j(scale * q[b,i,h,:] . k[b,j,h,:]) . v[b, :, h, :]

@@ -322,6 +322,54 @@ void oracle_rope_attention(const float* q, const float* k, const float* v, const
   free(kr);
 }
 
+/* image_proc.rs:57-96 (resize_normalize): PIL-style antialiased triangle filter. */
+static float tri_weight(float x) {
+  x = fabsf(x);
+  return x < 1.0f ? 1.0f - x : 0.0f;
+}
+
+/* image_proc.rs:57-96: one task per (channel, output row); rows >= nh and columns >= nw stay 0. Every
+ * step rounds in f32 in the reference's order (this file is built without FMA contraction): the tap
+ * span from truncating casts, the weight sums in tap order, r = sum_xx w(xx) * px row by row,
+ * acc += wy * r, then (acc / (wsx * wsy) - mean) / std. */
+void oracle_preprocess(const uint8_t* img, int h, int w, int nh, int nw, int size, const float* mean,
+                       const float* std_dev, float* out, int nthreads) {
+  const float sx = (float)w / (float)nw, sy = (float)h / (float)nh;
+  const float fx = sx > 1.0f ? sx : 1.0f, fy = sy > 1.0f ? sy : 1.0f;
+  memset(out, 0, sizeof(float) * 3 * (size_t)size * size);
+  const long rows = 3L * size;
+#pragma omp parallel for schedule(dynamic, 8) num_threads(threads_or_all(nthreads))
+  for (long i = 0; i < rows; ++i) {
+    const int c = (int)(i / size), y = (int)(i % size);
+    if (y >= nh) continue;
+    float* row = out + i * size;
+    const float cy = ((float)y + 0.5f) * sy;
+    long y0 = (long)(cy - fy + 0.5f);
+    if (y0 < 0) y0 = 0;
+    long y1 = (long)(cy + fy + 0.5f);
+    if (y1 > h) y1 = h;
+    float wsy = 0.0f;
+    for (long yy = y0; yy < y1; ++yy) wsy += tri_weight(((float)yy + 0.5f - cy) / fy);
+    for (int x = 0; x < nw && x < size; ++x) {
+      const float cx = ((float)x + 0.5f) * sx;
+      long x0 = (long)(cx - fx + 0.5f);
+      if (x0 < 0) x0 = 0;
+      long x1 = (long)(cx + fx + 0.5f);
+      if (x1 > w) x1 = w;
+      float wsx = 0.0f;
+      for (long xx = x0; xx < x1; ++xx) wsx += tri_weight(((float)xx + 0.5f - cx) / fx);
+      float acc = 0.0f;
+      for (long yy = y0; yy < y1; ++yy) {
+        float r = 0.0f;
+        for (long xx = x0; xx < x1; ++xx)
+          r += tri_weight(((float)xx + 0.5f - cx) / fx) * (float)img[(yy * w + xx) * 3 + c];
+        acc += tri_weight(((float)yy + 0.5f - cy) / fy) * r;
+      }
+      row[x] = (acc / (wsx * wsy) - mean[c]) / std_dev[c];
+    }
+  }
+}
+
 /* IEEE binary16 round-to-nearest-even, returned as f32 (gcc has no _Float16 on x86 here). */
 static float round_to_f16(float x) {
   if (isnan(x)) return x;

@@ -10,7 +10,8 @@
  * means "all OpenMP threads". Every function cites the reference lines it restates.
  *
  * Parity pins (see tests/test_oracle.py): each function is checked against an independent float64
- * formulation (textbook SAM decomposed rel-pos, torch grid_sample, torch sdpa, complex-number RoPE),
+ * formulation (textbook SAM decomposed rel-pos, torch grid_sample, torch sdpa, complex-number RoPE,
+ * PIL's float-mode bilinear resize),
  * closed forms and brute force on tiny inputs; none is left unpinned.
  */
 #ifndef SAM_ORACLE_H
@@ -59,6 +60,12 @@ void oracle_rope(const float* x, const float* cos_t, const float* sin_t, float* 
  * n_exclude keys left as they are, then sdpa with one head. cos/sin have `trows` rows. */
 void oracle_rope_attention(const float* q, const float* k, const float* v, const float* cos_t, const float* sin_t,
                            int trows, float* out, int lq, int mk, int d, int n_exclude, int nthreads);
+
+/* image_proc.rs:57-96 (resize_normalize; the CPU side of image_proc::prepare / prepare_square,
+ * image_proc.rs:21-53): antialiased triangle-filter resize of img (u8 [h, w, 3]) to nh x nw, then
+ * (x - mean[c]) / std[c], zero padded into out [3, size, size]. */
+void oracle_preprocess(const unsigned char* img, int h, int w, int nh, int nw, int size, const float* mean,
+                       const float* std_dev, float* out, int nthreads);
 
 /* Round-to-nearest-even conversions used to pre-round inputs to the kernel dtype
  * (the reference test does the same, tests/kernels.rs:28-31). */

@@ -47,6 +47,7 @@ def lib():
         L.oracle_rope_tables.argtypes = [ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_float, _F, _F]
         L.oracle_rope.argtypes = [_F, _F, _F, _F, ctypes.c_long, ctypes.c_int]
         L.oracle_rope_attention.argtypes = [_F, _F, _F, _F, _F, ctypes.c_int, _F] + [ctypes.c_int] * 5
+        L.oracle_preprocess.argtypes = [ctypes.c_void_p] + [ctypes.c_int] * 5 + [_F, _F, _F, ctypes.c_int]
         L.oracle_round_f16.argtypes = [_F, ctypes.c_long]
         L.oracle_round_bf16.argtypes = [_F, ctypes.c_long]
         L.oracle_randn.argtypes = [ctypes.c_ulonglong, _F, ctypes.c_long, ctypes.c_float, ctypes.c_float]
@@ -160,6 +161,29 @@ def rope_attention(q, k, v, cos, sin, n_exclude: int, nthreads: int = 0) -> np.n
     out = np.empty_like(q)
     lib().oracle_rope_attention(_p(q), _p(k), _p(v), _p(cos), _p(sin), trows, _p(out), lq, mk, d, n_exclude,
                                 nthreads)
+    return out
+
+
+SAM_MEAN = (123.675, 116.28, 103.53)  # image_proc.rs:7-8
+SAM_STD = (58.395, 57.12, 57.375)
+
+
+def resized_hw(h: int, w: int, size: int):
+    """image_proc.rs:22-25: the longest side scaled to `size`, rounded half up, in f32."""
+    scale = np.float32(size) / np.float32(max(w, h))
+    nw = int(np.float32(np.float32(w) * scale) + np.float32(0.5))
+    nh = int(np.float32(np.float32(h) * scale) + np.float32(0.5))
+    return nh, nw
+
+
+def preprocess(img, nh: int, nw: int, size: int, mean=SAM_MEAN, std=SAM_STD, nthreads: int = 0) -> np.ndarray:
+    """image_proc.rs:57-96: u8 [h, w, 3] -> f32 [3, size, size] (resize to nh x nw, normalise, zero pad)."""
+    img = np.ascontiguousarray(img, dtype=np.uint8)
+    h, w, c = img.shape
+    assert c == 3 and 1 <= nh <= size and 1 <= nw <= size
+    out = np.empty((3, size, size), np.float32)
+    m, sd = _f32(mean), _f32(std)
+    lib().oracle_preprocess(img.ctypes.data, h, w, nh, nw, size, _p(m), _p(sd), _p(out), nthreads)
     return out
 
 

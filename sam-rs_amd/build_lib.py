@@ -23,6 +23,7 @@ SOURCES = [
     "attn_relpos_win.hip", "attn_relpos_glob.hip",
     "attn_relpos_f32.hip",
     "deform_attn.hip",
+    "preprocess.hip",
     "relpos_softmax.hip",
     "qkv_split.hip",
     "flash_attn.hip", "flash_attn_d256.hip",

@@ -21,6 +21,9 @@ hipError_t relpos_softmax(int dtype, const void* s, const void* q, const void* t
                           int hd, float scale, hipStream_t stream);
 hipError_t qkv_split(int dtype, const void* y, const void* bias, void* out, long tokens, int n, int nh, int hd,
                      hipStream_t stream);
+hipError_t preprocess(int dtype, const void* img, void* out, int h, int w, int nh, int nw, int size, const float* mean,
+                      const float* stdv, hipStream_t stream);
+int preprocess_max_taps(int n, int nout);
 }  // namespace samhip
 
 namespace {
@@ -98,6 +101,27 @@ int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, vo
   hipError_t e = samhip::deform_attn(dtype, value, loc, attn, out, b, s, q, h, d, l, p, shapes,
                                      reinterpret_cast<hipStream_t>(stream));
   return check_launch(e, "deform-attn");
+}
+
+int sam_hip_preprocess(const void* img, void* out, int dtype, int h, int w, int nh, int nw, int size,
+                       const float* mean, const float* std_dev, void* stream) {
+  if (!img || !out || !mean || !std_dev) return fail(SAM_HIP_EINVAL, "preprocess: null pointer argument");
+  if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
+  if (h <= 0 || w <= 0 || size <= 0)
+    return fail(SAM_HIP_EINVAL, "preprocess: sizes must be positive (h=%d w=%d size=%d)", h, w, size);
+  if (nh < 1 || nw < 1 || nh > size || nw > size)
+    return fail(SAM_HIP_EINVAL, "preprocess: resized %dx%d does not fit in %dx%d", nh, nw, size, size);
+  if ((long)h * w * 3 >= (1L << 31) || 3L * size * size >= (1L << 31))
+    return fail(SAM_HIP_EUNSUPPORTED, "preprocess: more than 2^31 input or output elements");
+  for (int c = 0; c < 3; ++c)
+    if (!(std_dev[c] != 0.f)) return fail(SAM_HIP_EINVAL, "preprocess: std[%d] is zero", c);
+  if (samhip::preprocess_max_taps(w, nw) > 64)
+    return fail(SAM_HIP_EUNSUPPORTED, "preprocess: shrinking %d columns to %d needs more than 64 filter taps", w, nw);
+  if (samhip::preprocess_max_taps(h, nh) > 64)
+    return fail(SAM_HIP_EUNSUPPORTED, "preprocess: shrinking %d rows to %d needs more than 64 filter taps", h, nh);
+  hipError_t e = samhip::preprocess(dtype, img, out, h, w, nh, nw, size, mean, std_dev,
+                                    reinterpret_cast<hipStream_t>(stream));
+  return check_launch(e, "preprocess");
 }
 
 int sam_hip_relpos_softmax(const void* s, const void* q, const void* table, void* out, int dtype, long rows, int h,

@@ -48,6 +48,9 @@ def load():
         L.sam_hip_attn_relpos.argtypes = [_vp] * 5 + [_i] * 5 + [_f, _vp]
         L.sam_hip_attn_relpos.restype = _i
         L.sam_hip_deform_attn.argtypes = [_vp] * 4 + [_i] * 8 + [ctypes.POINTER(ctypes.c_int), _vp]
+        _fp = ctypes.POINTER(ctypes.c_float)
+        L.sam_hip_preprocess.argtypes = [_vp, _vp] + [_i] * 6 + [_fp, _fp, _vp]
+        L.sam_hip_preprocess.restype = _i
         L.sam_hip_deform_attn.restype = _i
         L.sam_hip_relpos_softmax.argtypes = [_vp] * 4 + [_i, ctypes.c_long, _i, _i, _i, _f, _vp]
         L.sam_hip_relpos_softmax.restype = _i
@@ -134,6 +137,56 @@ def deform_attn(value: torch.Tensor, loc: torch.Tensor, attn: torch.Tensor, shap
     _check(load().sam_hip_deform_attn(value.data_ptr(), loc.data_ptr(), attn.data_ptr(), out.data_ptr(), dt, b, s, q,
                                       h, d, l, p, flat, _stream()))
     return out
+
+
+IMG_SIZE = 1024  # image_proc.rs:6
+SAM_MEAN = (123.675, 116.28, 103.53)  # image_proc.rs:7-8
+SAM_STD = (58.395, 57.12, 57.375)
+
+
+def preprocess(src: torch.Tensor, new_hw, size: int, mean=SAM_MEAN, std=SAM_STD,
+               dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """kernels::preprocess (kernels.rs:1063-1070): src u8 [h, w, 3] on the device -> [1, 3, size, size]
+    of `dtype`: antialiased resize to new_hw = (nh, nw), (x - mean) / std, zero padding."""
+    if not src.is_cuda or src.dtype != torch.uint8 or src.dim() != 3 or src.shape[2] != 3:
+        raise SamHipError(f"preprocess: src must be a u8 [h, w, 3] device tensor, got {src.dtype} "
+                          f"{tuple(src.shape)}")
+    _contig(src)
+    if dtype not in _DTYPES:
+        raise SamHipError(f"unsupported dtype {dtype} for a sam-rs HIP kernel")
+    h, w, _ = src.shape
+    nh, nw = (int(x) for x in new_hw)
+    out = torch.empty((1, 3, size, size), dtype=dtype, device=src.device)
+    m = (ctypes.c_float * 3)(*[float(x) for x in mean])
+    sd = (ctypes.c_float * 3)(*[float(x) for x in std])
+    _check(load().sam_hip_preprocess(src.data_ptr(), out.data_ptr(), _DTYPES[dtype], h, w, nh, nw, size, m, sd,
+                                     _stream()))
+    return out
+
+
+def resized_hw(h: int, w: int, size: int = IMG_SIZE):
+    """image_proc.rs:22-25: the longest side scaled to `size`, computed in f32, rounded half up."""
+    import numpy as np
+
+    f = np.float32
+    scale = f(size) / f(max(w, h))
+    nw = int(f(w) * scale + f(0.5))
+    nh = int(f(h) * scale + f(0.5))
+    return nh, nw, float(scale)
+
+
+def prepare(src: torch.Tensor, size: int = IMG_SIZE, mean=SAM_MEAN, std=SAM_STD, dtype: torch.dtype = torch.float32):
+    """image_proc::prepare (image_proc.rs:21-36) for an image already on the device: resize the longest
+    side to `size`, normalise, pad. Returns (tensor [1, 3, size, size], orig (h, w), resized (nh, nw),
+    scale)."""
+    h, w = int(src.shape[0]), int(src.shape[1])
+    nh, nw, scale = resized_hw(h, w, size)
+    return preprocess(src, (nh, nw), size, mean, std, dtype), (h, w), (nh, nw), scale
+
+
+def prepare_square(src: torch.Tensor, size: int, mean=SAM_MEAN, std=SAM_STD, dtype: torch.dtype = torch.float32):
+    """image_proc::prepare_square (image_proc.rs:43-53): squash to size x size (no padding)."""
+    return preprocess(src, (size, size), size, mean, std, dtype)
 
 
 def relpos_softmax(scores: torch.Tensor, q: torch.Tensor, table: torch.Tensor, h: int, w: int,

@@ -335,3 +335,65 @@ def test_randn_is_seeded_and_normal(oracle_lib):
     c = oracle_lib.randn(8, (100000,))
     assert np.array_equal(a, b) and not np.array_equal(a, c)
     assert abs(a.mean()) < 0.02 and abs(a.std() - 1) < 0.02
+
+
+# ---- image preprocessing (image_proc.rs:57-96)
+
+PREP_CASES = [(1080, 1920, 1024), (480, 640, 1024), (37, 53, 64), (300, 200, 96), (1000, 9, 128), (5, 7, 16)]
+
+
+def _image(h, w, seed):
+    return _rng(seed).integers(0, 256, (h, w, 3), dtype=np.uint8)
+
+
+def _pil_preprocess(img, nh, nw, size, mean, std):
+    """PIL's own antialiased bilinear resize of each channel as a 32-bit float image (double
+    accumulation, normalised weights per pass), then (x - mean) / std and zero padding."""
+    from PIL import Image
+
+    out = np.zeros((3, size, size), np.float64)
+    for c in range(3):
+        ch = Image.fromarray(img[:, :, c].astype(np.float32), mode="F")
+        res = np.asarray(ch.resize((nw, nh), Image.BILINEAR), dtype=np.float64)
+        out[c, :nh, :nw] = (res - mean[c]) / std[c]
+    return out
+
+
+@pytest.mark.parametrize("h,w,size", PREP_CASES)
+def test_preprocess_matches_pil_float_resize(oracle_lib, h, w, size):
+    img = _image(h, w, h * 31 + w)
+    nh, nw = oracle_lib.resized_hw(h, w, size)
+    got = oracle_lib.preprocess(img, nh, nw, size)
+    want = _pil_preprocess(img, nh, nw, size, oracle_lib.SAM_MEAN, oracle_lib.SAM_STD)
+    assert np.abs(got - want).max() < 2e-5
+    # a transposed image, or swapped output axes, is far off
+    assert np.abs(oracle_lib.preprocess(img[::-1], nh, nw, size) - want).max() > 0.1
+
+
+def test_preprocess_resized_hw_is_the_longest_side_rule(oracle_lib):
+    assert oracle_lib.resized_hw(1080, 1920, 1024) == (576, 1024)
+    assert oracle_lib.resized_hw(480, 640, 1024) == (768, 1024)
+    assert oracle_lib.resized_hw(1365, 2048, 1024) == (683, 1024)  # 682.5 rounds half up
+    assert oracle_lib.resized_hw(2048, 1365, 1024) == (1024, 683)
+
+
+def test_preprocess_same_size_is_an_exact_normalisation(oracle_lib):
+    """nh = h and nw = w: each output pixel's filter is one tap of weight 1, so the result is exactly
+    (px - mean) / std in f32."""
+    img = _image(23, 41, 5)
+    got = oracle_lib.preprocess(img, 23, 41, 48)
+    m = np.array(oracle_lib.SAM_MEAN, np.float32)[:, None, None]
+    s = np.array(oracle_lib.SAM_STD, np.float32)[:, None, None]
+    want = (img.transpose(2, 0, 1).astype(np.float32) - m) / s
+    assert np.array_equal(got[:, :23, :41], want)
+    assert not got[:, 23:, :].any() and not got[:, :, 41:].any()
+
+
+def test_preprocess_constant_image_and_padding(oracle_lib):
+    img = np.full((90, 70, 3), 200, np.uint8)
+    img[..., 1] = 17
+    nh, nw = oracle_lib.resized_hw(90, 70, 32)
+    got = oracle_lib.preprocess(img, nh, nw, 32, mean=(1.0, 2.0, 3.0), std=(2.0, 4.0, 8.0))
+    for c, (v, m, s) in enumerate(zip((200, 17, 200), (1.0, 2.0, 3.0), (2.0, 4.0, 8.0))):
+        assert np.allclose(got[c, :nh, :nw], (v - m) / s, rtol=1e-6, atol=1e-6)
+        assert not got[c, nh:, :].any() and not got[c, :, nw:].any()
