@@ -250,6 +250,31 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
                 "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             }
 
+    # The elementwise steps beside attention in a ViT-H block, f16: the projection output plus bias plus
+    # the residual (4096 tokens x 1280), and the MLP's bias + exact GELU (4096 x 5120).
+    for name, (rows, cols) in (("bias_residual", (4096, 1280)), ("bias_gelu", (4096, 5120))):
+        y = torch.randn(rows, cols, device=dev, generator=g).half()
+        resid = torch.randn(rows, cols, device=dev, generator=g).half()
+        bvec = torch.randn(cols, device=dev, generator=g).half()
+        out = torch.empty_like(y)
+        if name == "bias_residual":
+            def run():
+                check(lib, lib.sam_hip_bias_residual(resid.data_ptr(), y.data_ptr(), bvec.data_ptr(), out.data_ptr(), 1,
+                                                     rows * cols, cols, sp))
+            nbytes = 3.0 * rows * cols * 2
+        else:
+            def run():
+                check(lib, lib.sam_hip_bias_gelu(y.data_ptr(), bvec.data_ptr(), out.data_ptr(), 1, rows * cols, cols,
+                                                 sp))
+            nbytes = 2.0 * rows * cols * 2
+        ms = timer.avg_ms(run, 50)
+        res[f"vit_h_{name}_f16"] = {
+            "workload": f"SAM ViT-H {name} over {rows} tokens x {cols} channels, f16",
+            "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+
     # SAM ViT-B encoder attention layers, f32 (12 heads x 64): window 300 x 14x14, global 12 x 64x64.
     for name, bh, hw in (("window", 300, 14), ("global", 12, 64)):
         n = hw * hw

@@ -90,6 +90,24 @@ int sam_hip_preprocess(const void* img, void* out, int dtype, int h, int w, int 
                        const float* mean, const float* std_dev, void* stream);
 
 /*
+ * out = res + y + bias[i % c] over `total` elements (bias broadcast over the last dimension, c of them),
+ * computed in f32 as (res + y) + bias and rounded once to `dtype`.
+ * Replaces kernels::bias_residual (kernels.rs:1040-1049; cuda::BiasResidual, kernels.rs:1229-1258,
+ * sam.cu:129-134; CPU cpu::BiasResidual, kernels.rs:618-640). Requires total % c == 0; total == 0 is a
+ * no-op. out may alias res or y.
+ */
+int sam_hip_bias_residual(const void* res, const void* y, const void* bias, void* out, int dtype, long total, int c,
+                          void* stream);
+
+/*
+ * out = gelu_erf(y + bias[i % c]) = 0.5 x (1 + erf(x / sqrt(2))) with x = y + bias[i % c], in f32, rounded
+ * once to `dtype`. Replaces kernels::bias_gelu (kernels.rs:1051-1061; cuda::BiasGelu,
+ * kernels.rs:1260-1290, sam.cu:136-141; CPU cpu::BiasGelu, kernels.rs:642-663). Requires
+ * total % c == 0. out may alias y.
+ */
+int sam_hip_bias_gelu(const void* y, const void* bias, void* out, int dtype, long total, int c, void* stream);
+
+/*
  * Flash attention without a mask, f16 / bf16, on [b, l, h, d] operands given by (batch, row, head)
  * element strides (NULL = contiguous [b, l, h, d]; the head dimension is always contiguous):
  *   out[b, i, h, :] = softmax_j(scale * q[b,i,h,:] . k[b,j,h,:]) . v[b, :, h, :]

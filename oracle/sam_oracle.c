@@ -370,6 +370,21 @@ void oracle_preprocess(const uint8_t* img, int h, int w, int nh, int nw, int siz
   }
 }
 
+/* kernels.rs:618-640 (cpu::BiasResidual): out[i] = res[i] + y[i] + b[i % c], left to right in f32. */
+void oracle_bias_residual(const float* res, const float* y, const float* b, float* out, long total, int c) {
+  for (long i = 0; i < total; ++i) out[i] = res[i] + y[i] + b[i % c];
+}
+
+/* kernels.rs:642-663 (cpu::BiasGelu): x = y[i] + b[i % c]; out = 0.5 * x * (1 + erf(x * FRAC_1_SQRT_2)).
+ * The reference calls the `libm` crate's erff (a port of musl's); this calls the C library's erff.
+ * Both are faithful to within an ulp, so the two can differ in the last bit of an element. */
+void oracle_bias_gelu(const float* y, const float* b, float* out, long total, int c) {
+  for (long i = 0; i < total; ++i) {
+    const float x = y[i] + b[i % c];
+    out[i] = 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+  }
+}
+
 /* IEEE binary16 round-to-nearest-even, returned as f32 (gcc has no _Float16 on x86 here). */
 static float round_to_f16(float x) {
   if (isnan(x)) return x;

@@ -67,6 +67,12 @@ void oracle_rope_attention(const float* q, const float* k, const float* v, const
 void oracle_preprocess(const unsigned char* img, int h, int w, int nh, int nw, int size, const float* mean,
                        const float* std_dev, float* out, int nthreads);
 
+/* kernels.rs:618-640 (cpu::BiasResidual): out = res + y + b[i % c]. */
+void oracle_bias_residual(const float* res, const float* y, const float* b, float* out, long total, int c);
+
+/* kernels.rs:642-663 (cpu::BiasGelu): out = gelu_erf(y + b[i % c]). */
+void oracle_bias_gelu(const float* y, const float* b, float* out, long total, int c);
+
 /* Round-to-nearest-even conversions used to pre-round inputs to the kernel dtype
  * (the reference test does the same, tests/kernels.rs:28-31). */
 void oracle_round_f16(float* x, long n);

@@ -48,6 +48,8 @@ def lib():
         L.oracle_rope.argtypes = [_F, _F, _F, _F, ctypes.c_long, ctypes.c_int]
         L.oracle_rope_attention.argtypes = [_F, _F, _F, _F, _F, ctypes.c_int, _F] + [ctypes.c_int] * 5
         L.oracle_preprocess.argtypes = [ctypes.c_void_p] + [ctypes.c_int] * 5 + [_F, _F, _F, ctypes.c_int]
+        L.oracle_bias_residual.argtypes = [_F, _F, _F, _F, ctypes.c_long, ctypes.c_int]
+        L.oracle_bias_gelu.argtypes = [_F, _F, _F, ctypes.c_long, ctypes.c_int]
         L.oracle_round_f16.argtypes = [_F, ctypes.c_long]
         L.oracle_round_bf16.argtypes = [_F, ctypes.c_long]
         L.oracle_randn.argtypes = [ctypes.c_ulonglong, _F, ctypes.c_long, ctypes.c_float, ctypes.c_float]
@@ -184,6 +186,24 @@ def preprocess(img, nh: int, nw: int, size: int, mean=SAM_MEAN, std=SAM_STD, nth
     out = np.empty((3, size, size), np.float32)
     m, sd = _f32(mean), _f32(std)
     lib().oracle_preprocess(img.ctypes.data, h, w, nh, nw, size, _p(m), _p(sd), _p(out), nthreads)
+    return out
+
+
+def bias_residual(res, y, bias) -> np.ndarray:
+    """kernels.rs:618-640: res + y + bias, bias broadcast over the last dimension."""
+    res, y, bias = _f32(res), _f32(y), _f32(bias).ravel()
+    assert res.shape == y.shape and res.size % bias.size == 0
+    out = np.empty_like(res)
+    lib().oracle_bias_residual(_p(res), _p(y), _p(bias), _p(out), res.size, bias.size)
+    return out
+
+
+def bias_gelu(y, bias) -> np.ndarray:
+    """kernels.rs:642-663: gelu_erf(y + bias), bias broadcast over the last dimension."""
+    y, bias = _f32(y), _f32(bias).ravel()
+    assert y.size % bias.size == 0
+    out = np.empty_like(y)
+    lib().oracle_bias_gelu(_p(y), _p(bias), _p(out), y.size, bias.size)
     return out
 
 

@@ -24,6 +24,7 @@ SOURCES = [
     "attn_relpos_f32.hip",
     "deform_attn.hip",
     "preprocess.hip",
+    "bias_ops.hip",
     "relpos_softmax.hip",
     "qkv_split.hip",
     "flash_attn.hip", "flash_attn_d256.hip",

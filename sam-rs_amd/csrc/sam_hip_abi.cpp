@@ -24,6 +24,9 @@ hipError_t qkv_split(int dtype, const void* y, const void* bias, void* out, long
 hipError_t preprocess(int dtype, const void* img, void* out, int h, int w, int nh, int nw, int size, const float* mean,
                       const float* stdv, hipStream_t stream);
 int preprocess_max_taps(int n, int nout);
+hipError_t bias_residual(int dtype, const void* res, const void* y, const void* b, void* out, long total, int c,
+                         hipStream_t stream);
+hipError_t bias_gelu(int dtype, const void* y, const void* b, void* out, long total, int c, hipStream_t stream);
 }  // namespace samhip
 
 namespace {
@@ -122,6 +125,25 @@ int sam_hip_preprocess(const void* img, void* out, int dtype, int h, int w, int 
   hipError_t e = samhip::preprocess(dtype, img, out, h, w, nh, nw, size, mean, std_dev,
                                     reinterpret_cast<hipStream_t>(stream));
   return check_launch(e, "preprocess");
+}
+
+int sam_hip_bias_residual(const void* res, const void* y, const void* bias, void* out, int dtype, long total, int c,
+                          void* stream) {
+  if (!res || !y || !bias || !out) return fail(SAM_HIP_EINVAL, "bias-residual: null pointer argument");
+  if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
+  if (total < 0 || c <= 0 || total % c != 0)
+    return fail(SAM_HIP_EINVAL, "bias-residual: %ld elements do not hold whole rows of the %d-element bias", total, c);
+  hipError_t e = samhip::bias_residual(dtype, res, y, bias, out, total, c, reinterpret_cast<hipStream_t>(stream));
+  return check_launch(e, "bias-residual");
+}
+
+int sam_hip_bias_gelu(const void* y, const void* bias, void* out, int dtype, long total, int c, void* stream) {
+  if (!y || !bias || !out) return fail(SAM_HIP_EINVAL, "bias-gelu: null pointer argument");
+  if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
+  if (total < 0 || c <= 0 || total % c != 0)
+    return fail(SAM_HIP_EINVAL, "bias-gelu: %ld elements do not hold whole rows of the %d-element bias", total, c);
+  hipError_t e = samhip::bias_gelu(dtype, y, bias, out, total, c, reinterpret_cast<hipStream_t>(stream));
+  return check_launch(e, "bias-gelu");
 }
 
 int sam_hip_relpos_softmax(const void* s, const void* q, const void* table, void* out, int dtype, long rows, int h,

@@ -48,6 +48,10 @@ def load():
         L.sam_hip_attn_relpos.argtypes = [_vp] * 5 + [_i] * 5 + [_f, _vp]
         L.sam_hip_attn_relpos.restype = _i
         L.sam_hip_deform_attn.argtypes = [_vp] * 4 + [_i] * 8 + [ctypes.POINTER(ctypes.c_int), _vp]
+        L.sam_hip_bias_residual.argtypes = [_vp] * 4 + [_i, ctypes.c_long, _i, _vp]
+        L.sam_hip_bias_residual.restype = _i
+        L.sam_hip_bias_gelu.argtypes = [_vp] * 3 + [_i, ctypes.c_long, _i, _vp]
+        L.sam_hip_bias_gelu.restype = _i
         _fp = ctypes.POINTER(ctypes.c_float)
         L.sam_hip_preprocess.argtypes = [_vp, _vp] + [_i] * 6 + [_fp, _fp, _vp]
         L.sam_hip_preprocess.restype = _i
@@ -136,6 +140,38 @@ def deform_attn(value: torch.Tensor, loc: torch.Tensor, attn: torch.Tensor, shap
     out = torch.empty((b, q, h * d), dtype=value.dtype, device=value.device)
     _check(load().sam_hip_deform_attn(value.data_ptr(), loc.data_ptr(), attn.data_ptr(), out.data_ptr(), dt, b, s, q,
                                       h, d, l, p, flat, _stream()))
+    return out
+
+
+def bias_residual(res: torch.Tensor, y: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """kernels::bias_residual (kernels.rs:1040-1049): res + y + bias, bias broadcast over the last
+    dimension; res and y of one shape, made contiguous first as the reference does."""
+    res, y, bias = res.contiguous(), y.contiguous(), bias.contiguous()
+    _contig(res, y, bias)
+    dt = _dtype(res, y, bias)
+    if res.shape != y.shape:
+        raise SamHipError(f"bias-residual: shape mismatch {tuple(res.shape)} vs {tuple(y.shape)}")
+    if bias.dim() != 1 or res.shape[-1] != bias.shape[0]:
+        raise SamHipError(f"bias-residual: bias {tuple(bias.shape)} does not match the last dimension of "
+                          f"{tuple(res.shape)}")
+    out = torch.empty_like(res)
+    _check(load().sam_hip_bias_residual(res.data_ptr(), y.data_ptr(), bias.data_ptr(), out.data_ptr(), dt,
+                                        res.numel(), bias.numel(), _stream()))
+    return out
+
+
+def bias_gelu(y: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """kernels::bias_gelu (kernels.rs:1051-1061): gelu_erf(y + bias), bias broadcast over the last
+    dimension."""
+    y, bias = y.contiguous(), bias.contiguous()
+    _contig(y, bias)
+    dt = _dtype(y, bias)
+    if bias.dim() != 1 or y.shape[-1] != bias.shape[0]:
+        raise SamHipError(f"bias-gelu: bias {tuple(bias.shape)} does not match the last dimension of "
+                          f"{tuple(y.shape)}")
+    out = torch.empty_like(y)
+    _check(load().sam_hip_bias_gelu(y.data_ptr(), bias.data_ptr(), out.data_ptr(), dt, y.numel(), bias.numel(),
+                                    _stream()))
     return out
 
 

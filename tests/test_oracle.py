@@ -397,3 +397,28 @@ def test_preprocess_constant_image_and_padding(oracle_lib):
     for c, (v, m, s) in enumerate(zip((200, 17, 200), (1.0, 2.0, 3.0), (2.0, 4.0, 8.0))):
         assert np.allclose(got[c, :nh, :nw], (v - m) / s, rtol=1e-6, atol=1e-6)
         assert not got[c, nh:, :].any() and not got[c, :, nw:].any()
+
+
+# ---- bias_residual and bias_gelu (kernels.rs:618-663)
+
+def test_bias_residual_is_the_left_to_right_f32_sum(oracle_lib):
+    r = _rng(3)
+    res, y = r.standard_normal((2, 7, 12)).astype(np.float32), r.standard_normal((2, 7, 12)).astype(np.float32)
+    b = r.standard_normal(12).astype(np.float32)
+    assert np.array_equal(oracle_lib.bias_residual(res, y, b), (res + y) + b)
+    assert not np.array_equal(oracle_lib.bias_residual(res, y, b), res + y + b[::-1])  # bias per column
+
+
+def test_bias_gelu_matches_float64_erf_and_its_limits(oracle_lib):
+    import math
+
+    r = _rng(4)
+    y = (3.0 * r.standard_normal((5, 40))).astype(np.float32)
+    b = r.standard_normal(40).astype(np.float32)
+    got = oracle_lib.bias_gelu(y, b)
+    x = (y + b).astype(np.float64)
+    want = 0.5 * x * (1.0 + np.vectorize(math.erf)(x / math.sqrt(2.0)))
+    assert np.allclose(got, want, rtol=2e-6, atol=1e-7)
+    big = np.array([[0.0, 12.0, -12.0, 1e-30]], np.float32)
+    out = oracle_lib.bias_gelu(big, np.zeros(4, np.float32))
+    assert out[0, 0] == 0.0 and out[0, 1] == 12.0 and out[0, 2] == 0.0 and out[0, 3] == np.float32(5e-31)
