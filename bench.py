@@ -250,6 +250,26 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
                 "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             }
 
+    # Encoder-level timing: the whole SAM image encoder (patch embedding, all blocks with their qkv / proj
+    # / MLP linears on hipBLASLt through torch, LayerNorms, the neck) on this library's attention,
+    # qkv_split, bias_residual and bias_gelu, f16, one 1024x1024 image; random-init weights N(0, 0.02).
+    # The reference's README gives 38 / 74 / 96 ms for these encoders on an RTX 4090 (f16, CUDA).
+    import sam_encoder
+
+    img = torch.randn(1, 3, 1024, 1024, device=dev, generator=g).half()
+    for name, cfg, readme_ms in (("vit_b", sam_encoder.VIT_B, 38.0), ("vit_l", sam_encoder.VIT_L, 74.0),
+                                 ("vit_h", sam_encoder.VIT_H, 96.0)):
+        wts = sam_encoder.random_weights(cfg, dtype=torch.float16, device=dev, seed=11)
+        with torch.no_grad():
+            ms = timer.avg_ms(lambda: sam_encoder.encoder_forward(img, wts), 10)
+        res[f"sam_{name}_encoder_f16"] = {
+            "workload": f"SAM {name.replace('_', '-').upper()} image encoder forward, 1024x1024, batch 1, f16 "
+                        f"({cfg.depth} blocks, dim {cfg.embed_dim}, {cfg.heads} heads)",
+            "ms": round(ms, 3), "readme_rtx4090_ms": readme_ms,
+            "note": "linears on torch/hipBLASLt, attention and elementwise steps on libsam_hip; synthetic weights",
+        }
+        del wts
+
     # The elementwise steps beside attention in a ViT-H block, f16: the projection output plus bias plus
     # the residual (4096 tokens x 1280), and the MLP's bias + exact GELU (4096 x 5120).
     for name, (rows, cols) in (("bias_residual", (4096, 1280)), ("bias_gelu", (4096, 5120))):

@@ -1,0 +1,165 @@
+"""SAM ViT image encoder forward on this library's kernels: the caller of the attention path.
+
+Mirrors sam1::encoder::ImageEncoder (sam1/encoder.rs:1-200): patch embedding, absolute position
+embedding, `depth` blocks (windowed 14x14 or global attention with decomposed rel-pos, MLP with exact
+GELU) and the neck. Per block, the reference's kernel calls map to:
+- qkv_split (kernels.rs:872) -> sam_hip.qkv_split;
+- attention_relpos / relpos_softmax + bmm (encoder.rs:79-82) -> sam_hip.attention_relpos (fused);
+- bias_residual (kernels.rs:1040) -> sam_hip.bias_residual;
+- bias_gelu (kernels.rs:1052) -> sam_hip.bias_gelu.
+
+The linears run as torch matmuls (hipBLASLt) and LayerNorm as torch's layer_norm. The two
+convolutions are exact GEMMs: the 16x16 stride-16 patch embedding over non-overlapping patches, and
+the neck's 3x3 conv as an unfold. Window partition zero-pads the token grid to a multiple of the
+window (encoder.rs:134-138): the padded tokens are real keys with no mask, whose q/k/v equal the qkv
+bias, as in the reference.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn.functional as F
+
+import sam_hip
+
+
+@dataclass(frozen=True)
+class EncoderConfig:
+    """encoder.rs:9-23."""
+    embed_dim: int
+    depth: int
+    heads: int
+    global_attn: tuple
+    window: int = 14
+    out_chans: int = 256
+    img_size: int = 1024
+    patch: int = 16
+
+
+VIT_B = EncoderConfig(768, 12, 12, (2, 5, 8, 11))
+VIT_L = EncoderConfig(1024, 24, 16, (5, 11, 17, 23))
+VIT_H = EncoderConfig(1280, 32, 16, (7, 15, 23, 31))
+
+
+@dataclass
+class BlockWeights:
+    norm1_w: torch.Tensor
+    norm1_b: torch.Tensor
+    qkv_wt: torch.Tensor  # [C, 3C] (the reference's Linear holds weight^T, encoder.rs:64)
+    qkv_b: torch.Tensor
+    proj_wt: torch.Tensor  # [C, C]
+    proj_b: torch.Tensor
+    rel: torch.Tensor  # rel_pos_h rows then rel_pos_w rows, [2 (2 input - 1), hd]
+    norm2_w: torch.Tensor
+    norm2_b: torch.Tensor
+    lin1_wt: torch.Tensor  # [C, 4C]
+    lin1_b: torch.Tensor
+    lin2_wt: torch.Tensor  # [4C, C]
+    lin2_b: torch.Tensor
+    window: int  # 0 = global attention
+
+
+@dataclass
+class EncoderWeights:
+    cfg: EncoderConfig
+    patch_wt: torch.Tensor  # [3 * 16 * 16, C], rows in (channel, ky, kx) order of the conv weight
+    patch_b: torch.Tensor
+    pos: torch.Tensor  # [1, 64, 64, C]
+    blocks: list = field(default_factory=list)
+    neck0_wt: torch.Tensor = None  # [C, out]
+    neck1_w: torch.Tensor = None
+    neck1_b: torch.Tensor = None
+    neck2_wt: torch.Tensor = None  # [out * 9, out], rows in (channel, ky, kx) order
+    neck3_w: torch.Tensor = None
+    neck3_b: torch.Tensor = None
+
+
+def random_weights(cfg: EncoderConfig, dtype=torch.float16, device="cuda", seed: int = 0, std: float = 0.02):
+    """Random-init weights of the architecture: N(0, std) for weights, tables and biases, LayerNorm
+    weight 1 and bias 0."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    c, hd = cfg.embed_dim, cfg.embed_dim // cfg.heads
+    grid = cfg.img_size // cfg.patch
+
+    def rn(*shape):
+        return (std * torch.randn(*shape, generator=g, device=device, dtype=torch.float32)).to(dtype)
+
+    def ones(n):
+        return torch.ones(n, device=device, dtype=dtype)
+
+    def zeros(n):
+        return torch.zeros(n, device=device, dtype=dtype)
+
+    w = EncoderWeights(cfg, rn(3 * cfg.patch * cfg.patch, c), rn(c), rn(1, grid, grid, c))
+    for i in range(cfg.depth):
+        glob = i in cfg.global_attn
+        inp = grid if glob else cfg.window
+        w.blocks.append(BlockWeights(ones(c), zeros(c), rn(c, 3 * c), rn(3 * c), rn(c, c), rn(c),
+                                     rn(2 * (2 * inp - 1), hd), ones(c), zeros(c), rn(c, 4 * c), rn(4 * c),
+                                     rn(4 * c, c), rn(c), 0 if glob else cfg.window))
+    o = cfg.out_chans
+    w.neck0_wt, w.neck1_w, w.neck1_b = rn(c, o), ones(o), zeros(o)
+    w.neck2_wt, w.neck3_w, w.neck3_b = rn(o * 9, o), ones(o), zeros(o)
+    return w
+
+
+def window_partition(x: torch.Tensor, ws: int):
+    """encoder.rs:129-137: [B, H, W, C] zero-padded to multiples of ws -> [B * nH * nW, ws, ws, C]."""
+    b, h, w, c = x.shape
+    ph, pw = (ws - h % ws) % ws, (ws - w % ws) % ws
+    if ph or pw:
+        x = F.pad(x, (0, 0, 0, pw, 0, ph))
+    hp, wp = h + ph, w + pw
+    x = x.view(b, hp // ws, ws, wp // ws, ws, c).permute(0, 1, 3, 2, 4, 5).reshape(-1, ws, ws, c)
+    return x, hp, wp
+
+
+def window_unpartition(x: torch.Tensor, ws: int, hp: int, wp: int, hw, b: int, c: int):
+    """encoder.rs:140-143."""
+    x = x.view(b, hp // ws, wp // ws, ws, ws, c).permute(0, 1, 3, 2, 4, 5).reshape(b, hp, wp, c)
+    return x[:, : hw[0], : hw[1], :].contiguous()
+
+
+def attention(x: torch.Tensor, p: BlockWeights, heads: int) -> torch.Tensor:
+    """encoder.rs:73-85: [nW, h, w, C] -> the output projection without its bias, [nW, h, w, C]."""
+    nw, h, w, c = x.shape
+    n, hd = h * w, c // heads
+    y = x.reshape(nw * n, c) @ p.qkv_wt
+    q, kt, v = sam_hip.qkv_split(y, p.qkv_b, n, heads, hd)
+    ctx = sam_hip.attention_relpos(q, kt, v, p.rel, h, w, hd ** -0.5)
+    out = ctx.view(nw, heads, n, hd).permute(0, 2, 1, 3).reshape(nw * n, c)
+    return (out @ p.proj_wt).view(nw, h, w, c)
+
+
+def block(x: torch.Tensor, p: BlockWeights, heads: int) -> torch.Tensor:
+    """encoder.rs:112-126."""
+    b, h, w, c = x.shape
+    y = F.layer_norm(x, (c,), p.norm1_w, p.norm1_b, 1e-6)
+    if p.window > 0:
+        parts, hp, wp = window_partition(y, p.window)
+        y = window_unpartition(attention(parts, p, heads), p.window, hp, wp, (h, w), b, c)
+    else:
+        y = attention(y, p, heads)
+    x = sam_hip.bias_residual(x, y, p.proj_b)
+    t = b * h * w
+    m = sam_hip.bias_gelu(F.layer_norm(x, (c,), p.norm2_w, p.norm2_b, 1e-6).reshape(t, c) @ p.lin1_wt, p.lin1_b)
+    return sam_hip.bias_residual(x, (m @ p.lin2_wt).view(b, h, w, c), p.lin2_b)
+
+
+def encoder_forward(img: torch.Tensor, w: EncoderWeights) -> torch.Tensor:
+    """encoder.rs:181-190: [1, 3, S, S] (the preprocess output) -> [1, out_chans, S/16, S/16]."""
+    cfg = w.cfg
+    b, _, s, _ = img.shape
+    g, k, c = s // cfg.patch, cfg.patch, cfg.embed_dim
+    patches = img.view(b, 3, g, k, g, k).permute(0, 2, 4, 1, 3, 5).reshape(b * g * g, 3 * k * k)
+    x = ((patches @ w.patch_wt) + w.patch_b).view(b, g, g, c) + w.pos
+    for p in w.blocks:
+        x = block(x, p, cfg.heads)
+    o = cfg.out_chans
+    y = x.reshape(b * g * g, c) @ w.neck0_wt  # 1x1 conv, tokens x out
+    y = F.layer_norm(y, (o,), w.neck1_w, w.neck1_b, 1e-6)  # LayerNorm2d over channels
+    cols = F.unfold(y.view(b, g, g, o).permute(0, 3, 1, 2), 3, padding=1)  # [b, o * 9, g * g]
+    y = cols.transpose(1, 2).reshape(b * g * g, o * 9) @ w.neck2_wt
+    y = F.layer_norm(y, (o,), w.neck3_w, w.neck3_b, 1e-6)
+    return y.view(b, g, g, o).permute(0, 3, 1, 2).contiguous()
