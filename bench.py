@@ -270,6 +270,26 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
         }
         del wts
 
+    # qkv_split of a ViT-H block (f16): the qkv projection's output [T, 3 x 1280] plus bias into q, kT, v
+    # for the 25 windows x 196 tokens of a windowed block (the grid padded to 70x70) and the 4096 tokens
+    # of a global block.
+    for name, (tok, n) in (("window", (4900, 196)), ("global", (4096, 4096))):
+        y = torch.randn(tok, 3 * 1280, device=dev, generator=g).half()
+        bq = torch.randn(3 * 1280, device=dev, generator=g).half()
+        packed = torch.empty(3, tok * 1280, device=dev, dtype=torch.float16)
+
+        def run():
+            check(lib, lib.sam_hip_qkv_split(y.data_ptr(), bq.data_ptr(), packed.data_ptr(), 1, tok, n, 16, 80, sp))
+
+        ms = timer.avg_ms(run, 50)
+        nbytes = 2.0 * tok * 3 * 1280 * 2
+        res[f"vit_h_qkv_split_{name}_f16"] = {
+            "workload": f"SAM ViT-H qkv_split, {tok} tokens ({n} per window) x 16 heads x 80, f16",
+            "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+
     # The elementwise steps beside attention in a ViT-H block, f16: the projection output plus bias plus
     # the residual (4096 tokens x 1280), and the MLP's bias + exact GELU (4096 x 5120).
     for name, (rows, cols) in (("bias_residual", (4096, 1280)), ("bias_gelu", (4096, 5120))):

@@ -65,7 +65,7 @@ def test_relpos_softmax_rejects_long_rows(hip):
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("n,nh,hd,win", [(196, 12, 64, 3), (196, 16, 80, 25), (4096, 16, 80, 1), (77, 3, 8, 2),
-                                         (5, 2, 6, 3)])
+                                         (5, 2, 6, 3), (130, 1, 256, 2), (64, 4, 16, 2), (65, 2, 24, 1)])
 def test_qkv_split_is_bit_exact(hip, n, nh, hd, win, dtype):
     print(f"qkv_split {dtype} n={n} nh={nh} hd={hd} win={win}", flush=True)
     r = np.random.default_rng(n + hd)
