@@ -96,3 +96,21 @@ def test_preprocess_errors(hip):
     tall = torch.zeros(4000, 2, 3, dtype=torch.uint8, device="cuda")
     with pytest.raises(hip.SamHipError, match="rows to 40 needs more than 64 filter taps"):
         hip.preprocess(tall, (40, 1), 64)
+
+
+def test_unaligned_image_and_strong_shrink(hip):
+    """An image that starts one byte into its allocation (the kernel gathers single bytes, so any
+    alignment works) and an 8000-row image shrunk 7.8x (31 taps per column)."""
+    h, w, size = 333, 517, 256
+    img = image(h, w, 12)
+    nh, nw = oracle.resized_hw(h, w, size)
+    buf = torch.zeros(h * w * 3 + 1, dtype=torch.uint8, device="cuda")
+    buf[1:] = torch.from_numpy(img.reshape(-1)).cuda()
+    src = buf[1:].view(h, w, 3)
+    assert src.data_ptr() % 4 != 0
+    got = hip.preprocess(src, (nh, nw), size)[0].cpu().numpy()
+    assert np.array_equal(got, oracle.preprocess(img, nh, nw, size))
+    big = image(8000, 600, 13)
+    nh, nw = oracle.resized_hw(8000, 600, 1024)
+    got = hip.preprocess(torch.from_numpy(big).cuda(), (nh, nw), 1024)[0].cpu().numpy()
+    assert np.array_equal(got, oracle.preprocess(big, nh, nw, 1024))
