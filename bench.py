@@ -96,8 +96,15 @@ def cpu_baseline():
     t_win = time_layer(WINDOWS * HEADS, 14, 14, 5)
     t_glob = time_layer(HEADS, 64, 64, 3)
     ms = 1e3 * ((DEPTH - len(GLOBAL_LAYERS)) * t_win + len(GLOBAL_LAYERS) * t_glob)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
     return {
         "value": round(ms, 1), "unit": "ms/image", "cores": cores, "kind": "port",
+        "cpu_model": model, "nproc": os.cpu_count(),
         "sample": "one windowed layer (400 x 14x14) and one global layer (16 x 64x64) of one image, f32, "
                   f"best of 5 and 3 runs ({t_win:.3f} s, {t_glob:.3f} s) scaled by 28 and 4 layers",
     }
