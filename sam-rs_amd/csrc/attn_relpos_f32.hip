@@ -24,13 +24,15 @@ template <int HDP> struct F32Geom {
   static constexpr int VSTR = MBO * 32 + 4;   // floats per V slot row
 };
 
+// Window grids (pair mode, 4 waves, hd <= 80) are held to 256 registers per lane, so that two
+// workgroups share a CU; the other shapes run one workgroup per CU.
 template <int HDP, int MODE, int NW>
-__global__ __launch_bounds__(NW * 64) void attn_relpos_f32_kernel(const float* __restrict__ q,
-                                                                 const float* __restrict__ kt,
-                                                                 const float* __restrict__ v,
-                                                                 const float* __restrict__ table,
-                                                                 float* __restrict__ out, int hd, int H, int W,
-                                                                 float scale) {
+constexpr int f32_min_blocks() { return (NW == 4 && MODE == kPair && HDP <= 80) ? 2 : 1; }
+
+template <int HDP, int MODE, int NW>
+__global__ __launch_bounds__(NW * 64, (f32_min_blocks<HDP, MODE, NW>())) void attn_relpos_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ kt, const float* __restrict__ v,
+    const float* __restrict__ table, float* __restrict__ out, int hd, int H, int W, float scale) {
   typedef KeyGeom<MODE> G;
   typedef F32Geom<HDP> FG;
   constexpr int HALF = FG::HALF, MBO = FG::MBO, KSTR = FG::KSTR, VSTR = FG::VSTR;
@@ -50,7 +52,8 @@ __global__ __launch_bounds__(NW * 64) void attn_relpos_f32_kernel(const float* _
   const int qidx = (blockIdx.x * NW + wave) * 32 + n;
   const bool qvalid = qidx < N;
   const int qi = qvalid ? qidx / W : 0, qj = qvalid ? qidx % W : 0;
-  float* rhs = rhs_base + wave * 64 * 32;
+  // this wave's bias scratch: one row of 32 per key row / column index, max(H, W) of them
+  float* rhs = rhs_base + wave * (H > W ? H : W) * 32;
 
   // Q fragments: lane supplies Q[query n][hh * HALF + s]
   float qf[HALF];
@@ -257,11 +260,15 @@ template <int HDP, int MODE, int NW>
 static hipError_t launch_f32(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                              int hd, int h, int w, float scale, hipStream_t stream) {
   typedef F32Geom<HDP> FG;
-  const size_t lds = (size_t)(2 * 64 * FG::KSTR + 2 * 64 * FG::VSTR + NW * 64 * 32) * sizeof(float);
+  // K and V double buffers, then max(h, w) scratch rows per wave: a 14x14 window needs 14 (two
+  // workgroups fit on a CU), a 64-column grid 64
+  const size_t tiles = (size_t)(2 * 64 * FG::KSTR + 2 * 64 * FG::VSTR) * sizeof(float);
+  const size_t lds = tiles + (size_t)NW * (h > w ? h : w) * 32 * sizeof(float);
   auto kern = attn_relpos_f32_kernel<HDP, MODE, NW>;
-  static bool attr_set = false;
+  static bool attr_set = false;  // one-time opt-in to the largest size this instantiation can ask for
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const int most = (int)(tiles + (size_t)NW * 64 * 32 * sizeof(float));
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, most);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
@@ -275,7 +282,8 @@ static hipError_t launch_f32(const void* q, const void* kt, const void* v, const
 template <int HDP, int MODE>
 static hipError_t f32_pick_nw(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                               int hd, int h, int w, float scale, hipStream_t stream) {
-  // LDS: two K and two V tiles of 64 x HDP floats plus 8 KB of Rh per wave must fit in 160 KB
+  // LDS: two K and two V tiles of 64 x HDP floats plus up to 8 KB of bias scratch per wave must fit in
+  // 160 KB
   if (HDP > 80) return launch_f32<HDP, MODE, 2>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   if (h * w > 1024) return launch_f32<HDP, MODE, 8>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   return launch_f32<HDP, MODE, 4>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
