@@ -257,6 +257,42 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
                 "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             }
 
+    # The encoder attention sweep (ViT-B / ViT-L / ViT-H, f16, batch 1 and 8): every attention layer of
+    # the encoder on fresh q/kT/v per layer, back to back, in ms per image. Windowed layers are
+    # batch x 25 windows x heads units of 14x14; global layers batch x heads 64x64 grids.
+    for mname, (depth, heads, hd, glob) in (("vit_b", (12, 12, 64, (2, 5, 8, 11))),
+                                            ("vit_l", (24, 16, 64, (5, 11, 17, 23))),
+                                            ("vit_h", (32, 16, 80, (7, 15, 23, 31)))):
+        for batch in (1, 8):
+            kinds = {}
+            for i in range(depth):
+                key = (batch * heads, 64) if i in glob else (batch * WINDOWS * heads, 14)
+                kinds[key] = kinds.get(key, 0) + 1
+            layer_us = {}
+            for (bh, side), count in kinds.items():
+                n = side * side
+                q = torch.randn(bh, n, hd, device=dev, generator=g).half()
+                kt = torch.randn(bh, hd, n, device=dev, generator=g).half()
+                v = torch.randn(bh, n, hd, device=dev, generator=g).half()
+                table = (0.02 * torch.randn(4 * side - 2, hd, device=dev, generator=g)).half()
+                out = torch.empty_like(q)
+
+                def run():
+                    check(lib, lib.sam_hip_attn_relpos(q.data_ptr(), kt.data_ptr(), v.data_ptr(), table.data_ptr(),
+                                                       out.data_ptr(), 1, bh, side, side, hd, hd ** -0.5, sp))
+
+                layer_us[side] = (timer.avg_ms(run, 10 if batch > 1 else 30) * 1e3, count, bh, n)
+                del q, kt, v, out
+            total_ms = sum(us * c for us, c, _, _ in layer_us.values()) / 1e3
+            gf = sum(flops(bh, n, hd) * c for _, c, bh, n in layer_us.values()) / 1e9
+            res[f"sweep_{mname}_attention_b{batch}_f16"] = {
+                "workload": f"SAM {mname.replace('_', '-').upper()} encoder attention, {depth} layers, {heads} heads x "
+                            f"{hd}, batch {batch}, f16",
+                "ms_per_image": round(total_ms / batch, 4),
+                "window_layer_us": round(layer_us[14][0], 2), "global_layer_us": round(layer_us[64][0], 2),
+                "tflops": round(gf / total_ms, 1),
+            }
+
     # Encoder-level timing: the whole SAM image encoder (patch embedding, all blocks with their qkv / proj
     # / MLP linears on hipBLASLt through torch, LayerNorms, the neck) on this library's attention,
     # qkv_split, bias_residual and bias_gelu, f16, one 1024x1024 image; random-init weights N(0, 0.02).
