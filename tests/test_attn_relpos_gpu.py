@@ -42,12 +42,13 @@ def run_gpu(hip, arrays, h, w, scale, dtype):
 
 # The reference test geometries (tests/kernels.rs:23, tests/cpu_gemm.rs:37) with its N(0,1) tables,
 # plus small and ragged shapes: a 2x3 grid with hd 8, a single grid row, and odd sizes; 64-column
-# grids with hd 80 of 1, 2, 3, 6 and 37 rows (ring shorter than its depth, odd tile counts, a partial
-# last query block); window grids with hd 80 of 13..16 rows (a full or half-empty last key tile, idle
-# query blocks).
+# grids with hd 80 and hd 64 of 1, 2, 3, 6 and 37 rows (ring shorter than its depth, odd tile counts, a
+# partial last query block); window grids with hd 80 of 13..16 rows (a full or half-empty last key
+# tile, idle query blocks).
 SMALL = [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (2, 3, 2, 8), (1, 5, 2, 16), (5, 33, 2, 32),
          (3, 40, 2, 128), (9, 17, 2, 48), (1, 64, 2, 80), (2, 64, 1, 80), (3, 64, 2, 80), (6, 64, 2, 80),
-         (37, 64, 3, 80), (16, 16, 2, 80), (13, 12, 3, 80), (15, 14, 2, 80), (14, 10, 2, 80)]
+         (37, 64, 3, 80), (16, 16, 2, 80), (13, 12, 3, 80), (15, 14, 2, 80), (14, 10, 2, 80),
+         (1, 64, 2, 64), (2, 64, 1, 64), (3, 64, 2, 64), (37, 64, 3, 64)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
@@ -60,6 +61,22 @@ def test_attention_relpos_reference_geometries(hip, h, w, bh, hd, dtype):
     want = oracle.attention_relpos(*arrays, h, w, scale)
     got = run_gpu(hip, arrays, h, w, scale, dtype)
     check(got, want, dtype, f"{h}x{w} bh={bh} hd={hd} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_vit_b_l_global_layer(hip, dtype):
+    """ViT-B / ViT-L global attention layer shape: 64x64 tokens, hd 64 (12 or 16 heads; 16 here),
+    q/k/v ~ N(0,1), rel_pos ~ N(0, 0.02). The GPU runs all 16 heads; the oracle checks heads 0, 9, 15."""
+    h = w = 64
+    bh, hd = 16, 64
+    print(f"vit-b/l global {dtype}", flush=True)
+    arrays = make_inputs(h, w, bh, hd, 17, dtype)
+    scale = hd ** -0.5
+    got = run_gpu(hip, arrays, h, w, scale, dtype)
+    heads = [0, 9, 15]
+    q, kt, v, table = arrays
+    want = oracle.attention_relpos(q[heads], kt[heads], v[heads], table, h, w, scale)
+    check(got[heads], want, dtype, f"vit-b/l global {dtype}")
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
