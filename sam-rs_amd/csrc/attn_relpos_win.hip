@@ -1,4 +1,5 @@
-// Fused rel-pos attention for the 14x14 windows of the SAM ViT (hd 80), f16 / bf16, for gfx950.
+// Fused rel-pos attention for the 14x14 windows of the SAM ViT (hd 80 for ViT-H, hd 64 for ViT-B and
+// ViT-L), f16 / bf16, for gfx950.
 //
 //   out[u, r, :] = softmax_k( scale * q[r] . k[k] + q[r] . Th[i - kh + H-1] + q[r] . Tw[j - kw + W-1] ) . v
 //
@@ -13,7 +14,7 @@
 // and there are only 400 of them per ViT-H layer. So the kernel is built for overlap between
 // workgroups rather than for a single one:
 //   * a workgroup of 4 waves takes half a unit (query blocks 0-3 or 4-7, one per wave) and needs
-//     70 KB of LDS, so two fit on a CU: one loads while the other computes, and the 800 half units
+//     70 KB (hd 80) or 57 KB (hd 64) of LDS, so two fit on a CU: one loads while the other computes, and the 800 half units
 //     fill the 512 workgroup slots of the chip in one and a half rounds instead of two full ones;
 //   * all data moves by LDS DMA (global_load_lds): the q rows, the table and tile 0 are requested at
 //     once, q into ring buffer 1 and the table into buffer 2, which tiles 1 and 2 take over once the
@@ -23,11 +24,14 @@
 //     memory operations complete in issue order), then one barrier publishes everyone's share;
 //   * kT tiles are stored [d][64 slots] with the 8-byte chunks of each row XOR-swizzled by the row's
 //     low bits, so the transpose reads (ds_read_b64_tr_b16) of four consecutive rows hit disjoint
-//     banks; V tiles are [64 slots][80]. The O^T rows 80..95 read past a slot's 80 columns and are
-//     discarded; the softmax denominator is summed on the VALU.
+//     banks; V tiles are [64 slots][hd]. hd 80: the O^T rows 80..95 read past a slot's 80 columns and
+//     are discarded. hd 64: the 8-byte chunks of slots 2, 3 (mod 4) are rotated by 8, so the transpose
+//     reads of four consecutive slots at a 128-byte pitch hit disjoint banks. The softmax denominator
+//     is summed on the VALU.
 // Padding keys (columns >= W, rows >= H) and padding table rows read valid data of the same tensor:
 // the keys' bias is -inf (P = 0), and the table rows' products are never scattered.
-// Limits (checked by the dispatcher): 13 <= H <= 16 (4 key tiles), W <= 16 and even, hd 80, scale > 0.
+// Limits (checked by the dispatcher): 13 <= H <= 16 (4 key tiles), W <= 16 and even, hd 80 or 64,
+// scale > 0.
 #include "lds_dma.hpp"
 #include "relpos_geom.hpp"
 
@@ -37,35 +41,42 @@ namespace win {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kHD = 80;        // head dim of this kernel
-constexpr int kKS = kHD / 16;  // k-steps of S^T = K Q^T
-constexpr int kMBO = 3;        // 32-row blocks of O^T (rows 80..95 are not stored)
-constexpr int kTiles = 4;      // key tiles per unit
-constexpr int kRing = 3;       // tile buffers
-constexpr int kTile = kHD * 64;                  // elements of a kT tile [d][64] and of a V tile [64][80]
-constexpr int kKDma = 3;                         // 1 KB units of a kT tile per wave (12 >= 10: 2 repeats)
-constexpr int kVDma = 3;                         // 1 KB units of a V tile per wave (12 >= 10: 2 repeats)
-constexpr int kTDma = kKDma + kVDma;             // DMAs per wave per tile
-constexpr int kQRows = kWaves * 32;              // q rows of a half unit
-constexpr int kQDma = kQRows * kHD * 2 / 1024 / kWaves;  // 1 KB units of q per wave: 5
-constexpr int kTRows = 64;                       // table rows in LDS: Th at [0, 32), Tw at [32, 64)
-constexpr int kTbDma = 3;                        // 1 KB units of the table per wave (12 >= 10: 2 repeats)
-constexpr int kRhsRows = 18;                     // per-wave bias scratch rows: -1 (junk), 0..15, 16 (junk)
+constexpr int kTiles = 4;          // key tiles per unit
+constexpr int kRing = 3;           // tile buffers
+constexpr int kQRows = kWaves * 32;  // q rows of a half unit
+constexpr int kTRows = 64;         // table rows in LDS: Th at [0, 32), Tw at [32, 64)
+constexpr int kRhsRows = 18;       // per-wave bias scratch rows: -1 (junk), 0..15, 16 (junk)
 constexpr float kSlack = 8.0f;
-static_assert(kQRows * kHD * 2 % (1024 * kWaves) == 0, "DMA split");
-static_assert(kTile * 2 <= kKDma * kWaves * 1024, "kT units");
-static_assert(kTile * 2 <= kVDma * kWaves * 1024 && kTRows * kHD * 2 <= kTbDma * kWaves * 1024, "units");
 
-// Buffer b is a kT tile at 2 b kTile and a V tile right after it; the last V tile is followed by 16
-// spare elements for the discarded O^T rows of its last slot; then the per-wave scratch. The q rows
-// fill buffer 1 and the table the kT half of buffer 2 until the prologue has read them.
-constexpr int kBuf = 2 * kTile;
-constexpr int kQOff = kBuf;
-constexpr int kTbOff = 2 * kBuf;
-constexpr int kRhsOff = kRing * kBuf + 16;
-constexpr size_t kLdsBytes = (size_t)kRhsOff * 2 + (size_t)kWaves * kRhsRows * 32 * sizeof(float);
-static_assert(kQRows * kHD <= kBuf && kTRows * kHD <= kTile, "staging fits buffers 1 and 2");
-static_assert(2 * kLdsBytes <= 160 * 1024, "two workgroups per CU");
+template <int HD> struct Shape {
+  static constexpr int kKS = HD / 16;            // k-steps of S^T = K Q^T
+  static constexpr int kMBO = (HD + 31) / 32;    // 32-row blocks of O^T (hd 80: rows 80..95 are not stored)
+  static constexpr int kTile = HD * 64;          // elements of a kT tile [d][64] and of a V tile [64][hd]
+  static constexpr int kUnits = HD / 8;          // 1 KB DMA units of a kT or V tile (and of the table)
+  static constexpr int kKDma = (kUnits + kWaves - 1) / kWaves;  // per wave: hd 80: 3 (2 repeats), hd 64: 2
+  static constexpr int kVDma = kKDma;
+  static constexpr int kTbDma = kKDma;
+  static constexpr int kTDma = kKDma + kVDma;    // DMAs per wave per tile
+  static constexpr int kQDma = kQRows * HD * 2 / 1024 / kWaves;  // 1 KB units of q per wave: 5 or 4
+  static constexpr int kChunks = HD / 4;         // 8-byte chunks of a V slot
+  // Buffer b is a kT tile at 2 b kTile and a V tile right after it; the last V tile is followed by 16
+  // spare elements for the discarded O^T rows of its last slot (hd 80); then the per-wave scratch.
+  // The q rows fill buffer 1 and the table the kT half of buffer 2 until the prologue has read them.
+  static constexpr int kBuf = 2 * kTile;
+  static constexpr int kQOff = kBuf;
+  static constexpr int kTbOff = 2 * kBuf;
+  static constexpr int kRhsOff = kRing * kBuf + 16;
+  static constexpr size_t kLdsBytes = (size_t)kRhsOff * 2 + (size_t)kWaves * kRhsRows * 32 * sizeof(float);
+  static_assert(HD == 80 || HD == 64, "head dims");
+  static_assert(kQRows * HD * 2 % (1024 * kWaves) == 0, "DMA split");
+  static_assert(kTile * 2 <= kKDma * kWaves * 1024 && kTRows * HD * 2 <= kTbDma * kWaves * 1024, "units");
+  static_assert(kQRows * HD <= kBuf && kTRows * HD <= kTile, "staging fits buffers 1 and 2");
+  static_assert(2 * kLdsBytes <= 160 * 1024, "two workgroups per CU");
+  // V chunk rotation: chunk c of slot r is stored at (c + vrot(r)) % kChunks
+  static constexpr int vrot(int r) { return HD == 64 && ((r >> 1) & 1) ? 8 : 0; }
+  // DMA unit of part i0 (parts past the last unit repeat the first ones)
+  static constexpr int unit(int i0) { return i0 < kUnits ? i0 : i0 - kUnits; }
+};
 
 // Chunk swizzle of kT rows: 8-byte chunk c of row d is stored at c ^ kswz(d & 3).
 __host__ __device__ constexpr int kswz(int r) { return 2 * (r & 1) + 8 * (r >> 1); }
@@ -77,7 +88,7 @@ __device__ __forceinline__ int win_xcd_block(int i, int total) {
   return x * per + (x < rem ? x : rem) + j;
 }
 
-template <typename T>
+template <typename T, int HD>
 __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const T* __restrict__ q,
                                                                        const T* __restrict__ kt,
                                                                        const T* __restrict__ v,
@@ -85,22 +96,24 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
                                                                        T* __restrict__ out, int H, int W,
                                                                        float scale) {
   using namespace win;
+  typedef Shape<HD> S;
+  constexpr int kKS = S::kKS, kMBO = S::kMBO, kTile = S::kTile, kBuf = S::kBuf, kTDma = S::kTDma;
   typedef KeyGeom<kPair> KG;
   typedef typename Vec<T>::x8 X8;
   constexpr bool kSplitP = __is_same(T, bf16);
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   T* kring = reinterpret_cast<T*>(smem);
-  T* tb = kring + kTbOff;
+  T* tb = kring + S::kTbOff;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: DMA destinations derive from it
-  float* rhs = reinterpret_cast<float*>(kring + kRhsOff) + wave * kRhsRows * 32;
+  float* rhs = reinterpret_cast<float*>(kring + S::kRhsOff) + wave * kRhsRows * 32;
   const unsigned lds0 = lds_addr(smem);
 
   const int N = H * W;
   const int lane = threadIdx.x & 63;
   const int n = lane & 31, hh = lane >> 5;
   const int g = lane >> 4, gi = lane & 15;
-  const long unit_elems = (long)N * kHD;
+  const long unit_elems = (long)N * HD;
   const int blk = win_xcd_block(blockIdx.x, gridDim.x);
   const long u = blk >> 1;
   const int q0 = (blk & 1) * kQRows;  // first query of this half unit
@@ -116,70 +129,62 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   // rows past H read other keys of the unit (their bias is -inf, so P = 0) or, past the unit's end, 0
   const i32x4 krsrc = buffer_rsrc(kt + u * unit_elems, (unsigned)(sizeof(T) * unit_elems));
   const i32x4 vrsrc = buffer_rsrc(v + u * unit_elems, (unsigned)(sizeof(T) * unit_elems));
-  unsigned kdof[kKDma], vdof[kVDma];
+  unsigned kdof[S::kKDma], vdof[S::kVDma];
 #pragma unroll
-  for (int p = 0; p < kKDma; ++p) {
+  for (int p = 0; p < S::kKDma; ++p) {
     // kT: unit i covers rows 8i .. 8i+7 of the tile, a lane 16 bytes (8 slots) of row 8i + lane/8: the
     // swizzle keeps 16-byte pairs of 8-byte chunks together, so they are the 8 consecutive slots
-    // from slot 4c = one grid row's columns kap .. kap+7 (kap = 0 or 8); units 10, 11 repeat 0, 1
-    const int i0 = wave + kWaves * p;
-    const int i = i0 < 10 ? i0 : i0 - 10;
+    // from slot 4c = one grid row's columns kap .. kap+7 (kap = 0 or 8); hd 80: units 10, 11 repeat 0, 1
+    const int i = S::unit(wave + kWaves * p);
     const int d = 8 * i + (lane >> 3);
     const int c = (2 * (lane & 7)) ^ kswz(d & 3);
     kdof[p] = (unsigned)(sizeof(T) * (d * N + (c >> 2) * W + 4 * (c & 3)));
   }
 #pragma unroll
-  for (int p = 0; p < kVDma; ++p) {
-    // V: unit j covers elements [512 j, 512 j + 512) of the [64 slots][80] tile, a lane 8 columns of
-    // one slot; units 10 and 11 repeat units 0 and 1
-    const int j0 = wave + kWaves * p;
-    const int j = j0 < 10 ? j0 : j0 - 10;
+  for (int p = 0; p < S::kVDma; ++p) {
+    // V: unit j covers elements [512 j, 512 j + 512) of the [64 slots][hd] tile, a lane 8 columns
+    // (two chunks, the rotation moves them together) of one slot; hd 80: units 10, 11 repeat 0, 1
+    const int j = S::unit(wave + kWaves * p);
     const int e = j * 512 + 8 * lane;
-    const int slot = e / kHD, col = e % kHD;
-    vdof[p] = (unsigned)(sizeof(T) * (((slot >> 4) * W + (slot & 15)) * kHD + col));
+    const int slot = e / HD, ch = (e % HD) >> 2;
+    const int col = 4 * ((ch + S::kChunks - S::vrot(slot)) % S::kChunks);
+    vdof[p] = (unsigned)(sizeof(T) * (((slot >> 4) * W + (slot & 15)) * HD + col));
   }
 
   // This wave's DMAs of K/V tile t (grid rows 4t .. 4t+3) into buffer buf (kTDma of them)
   auto tile_dma = [&](int t, int buf) {
-    const unsigned kso = (unsigned)(sizeof(T) * 4 * t * W), vso = kso * kHD;
+    const unsigned kso = (unsigned)(sizeof(T) * 4 * t * W), vso = kso * HD;
 #pragma unroll
-    for (int p = 0; p < kKDma; ++p) {
-      const int i0 = wave + kWaves * p;
-      const int i = i0 < 10 ? i0 : i0 - 10;
-      bdma16s(krsrc, kdof[p], kso, lds0 + (buf * kBuf + i * 512) * 2);
-    }
+    for (int p = 0; p < S::kKDma; ++p)
+      bdma16s(krsrc, kdof[p], kso, lds0 + (buf * kBuf + S::unit(wave + kWaves * p) * 512) * 2);
 #pragma unroll
-    for (int p = 0; p < kVDma; ++p) {
-      const int j0 = wave + kWaves * p;
-      const int j = j0 < 10 ? j0 : j0 - 10;
-      bdma16s(vrsrc, vdof[p], vso, lds0 + (buf * kBuf + kTile + j * 512) * 2);
-    }
+    for (int p = 0; p < S::kVDma; ++p)
+      bdma16s(vrsrc, vdof[p], vso, lds0 + (buf * kBuf + kTile + S::unit(wave + kWaves * p) * 512) * 2);
   };
 
   // ---- 1. the half unit's q rows, the table and tile 0, all requested at once
   {
     const char* base = reinterpret_cast<const char*>(q + u * unit_elems);
 #pragma unroll
-    for (int p = 0; p < kQDma; ++p) {
-      const int i = wave * kQDma + p;  // unit i covers q-image elements [512 i, 512 i + 512)
+    for (int p = 0; p < S::kQDma; ++p) {
+      const int i = wave * S::kQDma + p;  // unit i covers q-image elements [512 i, 512 i + 512)
       const int e = i * 512 + 8 * lane;
-      const int row = e / kHD, col = e % kHD;
+      const int row = e / HD, col = e % HD;
       const int src = q0 + row;  // queries past the end read query 0
-      dma16(base, (unsigned)(sizeof(T) * ((src < N ? src : 0) * kHD + col)), lds0 + (kQOff + i * 512) * 2);
+      dma16(base, (unsigned)(sizeof(T) * ((src < N ? src : 0) * HD + col)), lds0 + (S::kQOff + i * 512) * 2);
     }
   }
   {
-    // LDS row r < 32 is Th row r, row 32 + r is Tw row r (rows past the end read row 0); units 10, 11
-    // repeat units 0, 1
+    // LDS row r < 32 is Th row r, row 32 + r is Tw row r (rows past the end read row 0); hd 80: units
+    // 10, 11 repeat units 0, 1
     const char* base = reinterpret_cast<const char*>(table);
 #pragma unroll
-    for (int p = 0; p < kTbDma; ++p) {
-      const int i0 = wave + kWaves * p;
-      const int i = i0 < 10 ? i0 : i0 - 10;
+    for (int p = 0; p < S::kTbDma; ++p) {
+      const int i = S::unit(wave + kWaves * p);
       const int e = i * 512 + 8 * lane;
-      const int r = e / kHD, col = e % kHD;
+      const int r = e / HD, col = e % HD;
       const int src = r < 32 ? (r < 2 * H - 1 ? r : 0) : (r - 32 < 2 * W - 1 ? 2 * H - 1 + r - 32 : 0);
-      dma16(base, (unsigned)(sizeof(T) * (src * kHD + col)), lds0 + (kTbOff + i * 512) * 2);
+      dma16(base, (unsigned)(sizeof(T) * (src * HD + col)), lds0 + (S::kTbOff + i * 512) * 2);
     }
   }
   tile_dma(0, 0);
@@ -195,15 +200,21 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
     koff[mb] = d * 64 + (((slot >> 2) ^ kswz(d & 3)) << 2);
   }
   // V^T (A operand of O^T): source lane (4*s + c) reads the slot of key 16*(w4&1) + 8*r + 4*(g>>1) + s of
-  // block w4>>1, columns 32*ob + 16*(g&1) + 4*c .. +3
-  int voff[4][2];
+  // block w4>>1, columns 32*ob + 16*(g&1) + 4*c .. +3 (logical chunk 8*ob + 4*(g&1) + c). hd 80 has no
+  // rotation, so block ob is 32 columns further; hd 64 keeps an offset per block (the rotation wraps).
+  constexpr int kVB = HD == 80 ? 1 : kMBO;
+  int voff[kVB][4][2];
 #pragma unroll
-  for (int w4 = 0; w4 < 4; ++w4)
+  for (int ob = 0; ob < kVB; ++ob)
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int ms = 16 * (w4 & 1) + 8 * r + 4 * (g >> 1) + (gi >> 2);
-      voff[w4][r] = KG::slot(w4 >> 1, ms) * kHD + 16 * (g & 1) + 4 * (gi & 3);
-    }
+    for (int w4 = 0; w4 < 4; ++w4)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int ms = 16 * (w4 & 1) + 8 * r + 4 * (g >> 1) + (gi >> 2);
+        const int slot = KG::slot(w4 >> 1, ms);
+        const int c = 8 * ob + 4 * (g & 1) + (gi & 3);
+        voff[ob][w4][r] = slot * HD + 4 * ((c + S::vrot(slot)) % S::kChunks);
+      }
   auto wave_sync = [&]() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -217,15 +228,15 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   X8 qf[kKS];
 #pragma unroll
   for (int s = 0; s < kKS; ++s)
-    qf[s] = *reinterpret_cast<const X8*>(kring + kQOff + (wave * 32 + n) * kHD + 16 * s + 8 * hh);
+    qf[s] = *reinterpret_cast<const X8*>(kring + S::kQOff + (wave * 32 + n) * HD + 16 * s + 8 * hh);
   f32x16 cinit;
   float rh[kTiles][2];
   {
     f32x16 gh = f32x16{}, gw = f32x16{};
 #pragma unroll
     for (int s = 0; s < kKS; ++s) {
-      const X8 ah = *reinterpret_cast<const X8*>(tb + n * kHD + 16 * s + 8 * hh);
-      const X8 aw = *reinterpret_cast<const X8*>(tb + (32 + n) * kHD + 16 * s + 8 * hh);
+      const X8 ah = *reinterpret_cast<const X8*>(tb + n * HD + 16 * s + 8 * hh);
+      const X8 aw = *reinterpret_cast<const X8*>(tb + (32 + n) * HD + 16 * s + 8 * hh);
       gh = mma32(ah, qf[s], gh);
       gw = mma32(aw, qf[s], gw);
     }
@@ -337,7 +348,8 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
     for (int w4 = 0; w4 < 2 * NB; ++w4) {
 #pragma unroll
       for (int ob = 0; ob < kMBO; ++ob) {
-        const X8 a = join8<T>(lds_read_tr16(vbuf + voff[w4][0] + 32 * ob), lds_read_tr16(vbuf + voff[w4][1] + 32 * ob));
+        const int vo = HD == 80 ? 32 * ob : 0, vb = HD == 80 ? 0 : ob;
+        const X8 a = join8<T>(lds_read_tr16(vbuf + voff[vb][w4][0] + vo), lds_read_tr16(vbuf + voff[vb][w4][1] + vo));
         o[ob] = mma32(a, b[w4], o[ob]);
         if (kSplitP) o[ob] = mma32(a, blo[w4], o[ob]);
       }
@@ -370,12 +382,12 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   // ---- 4. normalise and store: lane holds O^T[32*ob + 8*a + 4*hh + b][query n]
   const float inv = 1.f / sum_with_partner32(l_run);
   if (qvalid) {
-    T* orow = out + u * unit_elems + qidx * kHD;
+    T* orow = out + u * unit_elems + qidx * HD;
 #pragma unroll
     for (int ob = 0; ob < kMBO; ++ob)
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        if (32 * ob + 8 * a < kHD) {
+        if (32 * ob + 8 * a < HD) {
           typename Vec<T>::x4 w4;
 #pragma unroll
           for (int bb = 0; bb < 4; ++bb) w4[bb] = from_f32<T>(o[ob][4 * a + bb] * inv);
@@ -387,29 +399,33 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
 
 // ---------------------------------------------------------------------------------------------- launch
 
-template <typename T>
+template <typename T, int HD>
 static hipError_t launch_win(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                              int h, int w, float scale, hipStream_t stream) {
-  auto kern = attn_relpos_win_kernel<T>;
+  auto kern = attn_relpos_win_kernel<T, HD>;
+  constexpr size_t lds = win::Shape<HD>::kLdsBytes;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e =
-        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)win::kLdsBytes);
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)(2 * bh)), dim3(win::kThreads), win::kLdsBytes, stream, (const T*)q,
+  hipLaunchKernelGGL(kern, dim3((unsigned)(2 * bh)), dim3(win::kThreads), lds, stream, (const T*)q,
                      (const T*)kt, (const T*)v, (const T*)table, (T*)out, h, w, scale);
   return hipGetLastError();
 }
 
-// The SAM windows (13 <= H <= 16 so a unit is exactly 4 key tiles, W <= 16 even, hd 80, scale > 0);
-// returns false (nothing launched) for shapes it does not take.
+// The SAM windows (13 <= H <= 16 so a unit is exactly 4 key tiles, W <= 16 even, hd 80 or 64,
+// scale > 0); returns false (nothing launched) for shapes it does not take.
 bool attn_relpos_window(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                         int hd, int h, int w, float scale, hipStream_t stream, hipError_t* err) {
-  if (hd != win::kHD || h < 13 || h > 16 || w > 16 || w % 2 != 0 || !(scale > 0.f)) return false;
-  *err = dtype == kF16 ? launch_win<f16>(q, kt, v, table, out, bh, h, w, scale, stream)
-                       : launch_win<bf16>(q, kt, v, table, out, bh, h, w, scale, stream);
+  if ((hd != 80 && hd != 64) || h < 13 || h > 16 || w > 16 || w % 2 != 0 || !(scale > 0.f)) return false;
+  if (hd == 80)
+    *err = dtype == kF16 ? launch_win<f16, 80>(q, kt, v, table, out, bh, h, w, scale, stream)
+                         : launch_win<bf16, 80>(q, kt, v, table, out, bh, h, w, scale, stream);
+  else
+    *err = dtype == kF16 ? launch_win<f16, 64>(q, kt, v, table, out, bh, h, w, scale, stream)
+                         : launch_win<bf16, 64>(q, kt, v, table, out, bh, h, w, scale, stream);
   return true;
 }
 

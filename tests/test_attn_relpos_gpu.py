@@ -43,12 +43,13 @@ def run_gpu(hip, arrays, h, w, scale, dtype):
 # The reference test geometries (tests/kernels.rs:23, tests/cpu_gemm.rs:37) with its N(0,1) tables,
 # plus small and ragged shapes: a 2x3 grid with hd 8, a single grid row, and odd sizes; 64-column
 # grids with hd 80 and hd 64 of 1, 2, 3, 6 and 37 rows (ring shorter than its depth, odd tile counts, a
-# partial last query block); window grids with hd 80 of 13..16 rows (a full or half-empty last key
-# tile, idle query blocks).
+# partial last query block); window grids with hd 80 and hd 64 of 13..16 rows (a full or half-empty
+# last key tile, idle query blocks).
 SMALL = [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (2, 3, 2, 8), (1, 5, 2, 16), (5, 33, 2, 32),
          (3, 40, 2, 128), (9, 17, 2, 48), (1, 64, 2, 80), (2, 64, 1, 80), (3, 64, 2, 80), (6, 64, 2, 80),
          (37, 64, 3, 80), (16, 16, 2, 80), (13, 12, 3, 80), (15, 14, 2, 80), (14, 10, 2, 80),
-         (1, 64, 2, 64), (2, 64, 1, 64), (3, 64, 2, 64), (37, 64, 3, 64)]
+         (1, 64, 2, 64), (2, 64, 1, 64), (3, 64, 2, 64), (37, 64, 3, 64), (16, 16, 2, 64), (13, 12, 3, 64),
+         (15, 14, 2, 64), (14, 10, 2, 64)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
@@ -106,6 +107,21 @@ def test_vit_h_window_layer(hip, dtype):
     want = oracle.attention_relpos(*arrays, h, w, scale)
     got = run_gpu(hip, arrays, h, w, scale, dtype)
     check(got, want, dtype, f"vit-h window {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("bh", [300, 400], ids=["vit_b", "vit_l"])
+def test_vit_b_l_window_layer(hip, bh, dtype):
+    """ViT-B (12 heads) and ViT-L (16 heads) windowed layers at batch 1: 25 windows x heads of 14x14
+    tokens, hd 64, (27, 64) tables."""
+    h = w = 14
+    hd = 64
+    print(f"vit-b/l window {dtype} bh={bh}", flush=True)
+    arrays = make_inputs(h, w, bh, hd, 9 + bh, dtype)
+    scale = hd ** -0.5
+    want = oracle.attention_relpos(*arrays, h, w, scale)
+    got = run_gpu(hip, arrays, h, w, scale, dtype)
+    check(got, want, dtype, f"vit-b/l window {dtype} bh={bh}")
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
