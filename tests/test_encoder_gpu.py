@@ -4,8 +4,9 @@ decomposed rel-pos attention, MLP with exact GELU, neck), on an MI355X.
 
 The reference here is the textbook form: full score matrices with get_rel_pos tables and an einsum
 bias, torch's softmax, conv2d for the patch embedding and the neck, no fused kernels. The small
-configuration (2 heads x hd 80, one windowed block on the 64x64 grid padded to 70x70, one global block)
-runs the same dedicated window and global kernels as ViT-H.
+configurations (2 heads x hd 80 or hd 64, one windowed block on the 64x64 grid padded to 70x70, one
+global block) run the same dedicated window and global kernels as ViT-H (hd 80) and ViT-B / ViT-L
+(hd 64).
 """
 import numpy as np
 import pytest
@@ -75,9 +76,10 @@ def ref_forward(img, w, enc):
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 2e-4), (torch.float16, 2e-2), (torch.bfloat16, 6e-2)],
                          ids=["f32", "f16", "bf16"])
-def test_small_encoder_matches_torch_float32(enc, dtype, tol):
-    print(f"encoder {dtype}", flush=True)
-    cfg = enc.EncoderConfig(160, 2, 2, (1,))
+@pytest.mark.parametrize("dim", [160, 128], ids=["hd80", "hd64"])
+def test_small_encoder_matches_torch_float32(enc, dim, dtype, tol):
+    print(f"encoder dim {dim} {dtype}", flush=True)
+    cfg = enc.EncoderConfig(dim, 2, 2, (1,))
     w = enc.random_weights(cfg, dtype=dtype, seed=3, std=0.05)
     g = torch.Generator(device="cuda").manual_seed(4)
     img = torch.randn(1, 3, 1024, 1024, generator=g, device="cuda").to(dtype)
