@@ -259,13 +259,13 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
                 "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             }
 
-    # The encoder attention sweep (ViT-B / ViT-L / ViT-H, f16, batch 1 and 8): every attention layer of
+    # The encoder attention sweep (ViT-B / ViT-L / ViT-H, f16, batch 1, 4 and 8): every attention layer of
     # the encoder on fresh q/kT/v per layer, back to back, in ms per image. Windowed layers are
     # batch x 25 windows x heads units of 14x14; global layers batch x heads 64x64 grids.
     for mname, (depth, heads, hd, glob) in (("vit_b", (12, 12, 64, (2, 5, 8, 11))),
                                             ("vit_l", (24, 16, 64, (5, 11, 17, 23))),
                                             ("vit_h", (32, 16, 80, (7, 15, 23, 31)))):
-        for batch in (1, 8):
+        for batch in (1, 4, 8):
             kinds = {}
             for i in range(depth):
                 key = (batch * heads, 64) if i in glob else (batch * WINDOWS * heads, 14)

@@ -14,8 +14,10 @@
 // and there are only 400 of them per ViT-H layer. So the kernel is built for overlap between
 // workgroups rather than for a single one:
 //   * a workgroup of 4 waves takes half a unit (query blocks 0-3 or 4-7, one per wave) and needs
-//     70 KB (hd 80) or 57 KB (hd 64) of LDS, so two fit on a CU: one loads while the other computes, and the 800 half units
-//     fill the 512 workgroup slots of the chip in one and a half rounds instead of two full ones;
+//     61 KB (hd 80) or 48 KB (hd 64) of LDS, so two (hd 80) or three (hd 64) fit on a CU: one loads
+//     while another computes, and the 800 half units of a ViT-H layer fill the 512 workgroup slots of
+//     the chip in one and a half rounds instead of two full ones (the 600 of a ViT-B layer fit the 768
+//     slots at hd 64 in one);
 //   * all data moves by LDS DMA (global_load_lds): the q rows, the table and tile 0 are requested at
 //     once, q into ring buffer 1 and the table into buffer 2, which tiles 1 and 2 take over once the
 //     bias prologue has read them; tile 3 then goes into buffer 0. The two halves of a unit are
@@ -60,18 +62,19 @@ template <int HD> struct Shape {
   static constexpr int kQDma = kQRows * HD * 2 / 1024 / kWaves;  // 1 KB units of q per wave: 5 or 4
   static constexpr int kChunks = HD / 4;         // 8-byte chunks of a V slot
   // Buffer b is a kT tile at 2 b kTile and a V tile right after it; the last V tile is followed by 16
-  // spare elements for the discarded O^T rows of its last slot (hd 80); then the per-wave scratch.
-  // The q rows fill buffer 1 and the table the kT half of buffer 2 until the prologue has read them.
+  // spare elements for the discarded O^T rows of its last slot (hd 80). The q rows fill buffer 1 and
+  // the table the kT half of buffer 2 until the prologue has read them; a wave's bias scratch then
+  // overlays its own 32 q rows, which it alone reads (into registers) before it scatters.
   static constexpr int kBuf = 2 * kTile;
   static constexpr int kQOff = kBuf;
   static constexpr int kTbOff = 2 * kBuf;
-  static constexpr int kRhsOff = kRing * kBuf + 16;
-  static constexpr size_t kLdsBytes = (size_t)kRhsOff * 2 + (size_t)kWaves * kRhsRows * 32 * sizeof(float);
+  static constexpr size_t kLdsBytes = (size_t)(kRing * kBuf + 16) * 2;
   static_assert(HD == 80 || HD == 64, "head dims");
+  static_assert(kRhsRows * 32 * sizeof(float) <= 32 * HD * 2, "the scratch fits in a wave's q rows");
+  static_assert((HD == 64 ? 3 : 2) * kLdsBytes <= 160 * 1024, "workgroups per CU");
   static_assert(kQRows * HD * 2 % (1024 * kWaves) == 0, "DMA split");
   static_assert(kTile * 2 <= kKDma * kWaves * 1024 && kTRows * HD * 2 <= kTbDma * kWaves * 1024, "units");
   static_assert(kQRows * HD <= kBuf && kTRows * HD <= kTile, "staging fits buffers 1 and 2");
-  static_assert(2 * kLdsBytes <= 160 * 1024, "two workgroups per CU");
   // V chunk rotation: chunk c of slot r is stored at (c + vrot(r)) % kChunks
   static constexpr int vrot(int r) { return HD == 64 && ((r >> 1) & 1) ? 8 : 0; }
   // DMA unit of part i0 (parts past the last unit repeat the first ones)
@@ -106,7 +109,8 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   T* kring = reinterpret_cast<T*>(smem);
   T* tb = kring + S::kTbOff;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: DMA destinations derive from it
-  float* rhs = reinterpret_cast<float*>(kring + S::kRhsOff) + wave * kRhsRows * 32;
+  // the bias scratch, wave-private, over this wave's q rows in buffer 1 (prologue only)
+  float* rhs = reinterpret_cast<float*>(kring + S::kQOff + wave * 32 * HD);
   const unsigned lds0 = lds_addr(smem);
 
   const int N = H * W;
