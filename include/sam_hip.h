@@ -10,7 +10,8 @@
  *   - stream: a hipStream_t passed as void* (NULL = the default stream); launches are asynchronous,
  *     exactly as the reference's are on candle's CUDA stream;
  *   - return 0 on success, nonzero on error; sam_hip_last_error() then returns a message (per thread);
- *   - no global mutable state beyond per-kernel one-time attribute set-up; safe to call from many threads.
+ *   - no global mutable state beyond each kernel's once-per-device LDS opt-in (an atomic flag word);
+ *     safe to call from many threads.
  */
 #ifndef SAM_HIP_H
 #define SAM_HIP_H

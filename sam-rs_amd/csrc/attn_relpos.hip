@@ -467,13 +467,11 @@ static hipError_t launch_attn(const void* q, const void* kt, const void* v, cons
   const int rows = h > w ? h : w;
   const size_t lds = tiles_lds_bytes<T, HDP, NBUF>() + (size_t)NWV * (rows + 1) * 32 * sizeof(float);
   auto kern = attn_relpos_kernel<T, HDP, MODE, VK, POS, NBUF, FULL, NWV>;
-  static bool attr_set = false;  // one-time opt-in to more than 64 KB of dynamic LDS
-  if (!attr_set) {
+  static std::atomic<unsigned long long> lds_done{0};  // opt-in to more than 64 KB of dynamic LDS
+  {
     const size_t max_lds = tiles_lds_bytes<T, HDP, NBUF>() + (size_t)NWV * 65 * 32 * sizeof(float);
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)(max_lds < 163840 ? max_lds : 163840));
+    const hipError_t e = lds_opt_in(lds_done, (const void*)kern, (int)(max_lds < 163840 ? max_lds : 163840));
     if (e != hipSuccess) return e;
-    attr_set = true;
   }
   const int n = h * w;
   const int qblocks = (n + NWV * 32 - 1) / (NWV * 32);  // NWV * 32 queries per workgroup

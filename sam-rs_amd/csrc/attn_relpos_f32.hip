@@ -265,12 +265,11 @@ static hipError_t launch_f32(const void* q, const void* kt, const void* v, const
   const size_t tiles = (size_t)(2 * 64 * FG::KSTR + 2 * 64 * FG::VSTR) * sizeof(float);
   const size_t lds = tiles + (size_t)NW * (h > w ? h : w) * 32 * sizeof(float);
   auto kern = attn_relpos_f32_kernel<HDP, MODE, NW>;
-  static bool attr_set = false;  // one-time opt-in to the largest size this instantiation can ask for
-  if (!attr_set) {
+  static std::atomic<unsigned long long> lds_done{0};  // opt-in to the largest size this instantiation asks for
+  {
     const int most = (int)(tiles + (size_t)NW * 64 * 32 * sizeof(float));
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, most);
+    const hipError_t e = lds_opt_in(lds_done, (const void*)kern, most);
     if (e != hipSuccess) return e;
-    attr_set = true;
   }
   const int n = h * w;
   dim3 grid((n + 32 * NW - 1) / (32 * NW), bh);

@@ -430,12 +430,8 @@ static hipError_t launch_glob(const void* q, const void* kt, const void* v, cons
                               int h, float scale, hipStream_t stream) {
   auto kern = attn_relpos_glob_kernel<T, HD>;
   constexpr size_t lds = glob::Shape<HD>::kLdsBytes;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<unsigned long long> lds_done{0};
+  if (const hipError_t e = lds_opt_in(lds_done, (const void*)kern, (int)lds); e != hipSuccess) return e;
   const int qblocks = (h * 64 + glob::kWaves * 32 - 1) / (glob::kWaves * 32);
   hipLaunchKernelGGL(kern, dim3((unsigned)(bh * qblocks)), dim3(glob::kThreads), lds, stream,
                      (const T*)q, (const T*)kt, (const T*)v, (const T*)table, (T*)out, h, scale, qblocks);

@@ -408,12 +408,8 @@ static hipError_t launch_win(const void* q, const void* kt, const void* v, const
                              int h, int w, float scale, hipStream_t stream) {
   auto kern = attn_relpos_win_kernel<T, HD>;
   constexpr size_t lds = win::Shape<HD>::kLdsBytes;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<unsigned long long> lds_done{0};
+  if (const hipError_t e = lds_opt_in(lds_done, (const void*)kern, (int)lds); e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3((unsigned)(2 * bh)), dim3(win::kThreads), lds, stream, (const T*)q,
                      (const T*)kt, (const T*)v, (const T*)table, (T*)out, h, w, scale);
   return hipGetLastError();

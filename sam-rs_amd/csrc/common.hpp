@@ -5,7 +5,23 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace samhip {
+
+// Opts kernel fn in to `bytes` of dynamic LDS on the current device, once per device (devices 0..63)
+// and process. `done` is the kernel's own flag word, one bit per device. Callers on several threads
+// may both make the call; repeating it is harmless, and the flag word is atomic.
+inline hipError_t lds_opt_in(std::atomic<unsigned long long>& done, const void* fn, int bytes) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const unsigned long long bit = 1ull << (dev & 63);
+  if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
 
 typedef _Float16 f16;
 typedef __bf16 bf16;

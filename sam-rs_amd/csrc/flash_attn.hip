@@ -383,12 +383,9 @@ static hipError_t launch_flash(FlashParams p, bool ropeq, hipStream_t stream) {
     e = flash256_launch(__is_same(T, f16) ? kF16 : kBF16, p, ropeq, stream);
   } else {
     auto kern = ropeq ? flash_fwd_kernel<T, DP, NW, true> : flash_fwd_kernel<T, DP, NW, false>;
-    static bool attr_set[2] = {false, false};  // one-time opt-in to more than 64 KB of dynamic LDS
-    if (!attr_set[ropeq]) {
-      e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)FG::LDS);
-      if (e != hipSuccess) return e;
-      attr_set[ropeq] = true;
-    }
+    static std::atomic<unsigned long long> lds_done[2];  // opt-in to more than 64 KB of dynamic LDS
+    e = lds_opt_in(lds_done[ropeq], (const void*)kern, (int)FG::LDS);
+    if (e != hipSuccess) return e;
     const long blocks = (long)p.b * p.h * p.qblocks * p.nsplit;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(FG::NT), FG::LDS, stream, p);
     e = hipGetLastError();

@@ -352,12 +352,8 @@ bool flash256_eligible(const FlashParams& p, int elem_bytes) {
 template <typename T>
 static hipError_t launch256(FlashParams p, bool ropeq, hipStream_t stream) {
   auto kern = ropeq ? flash256_kernel<T, true> : flash256_kernel<T, false>;
-  static bool attr_set[2] = {false, false};  // one-time opt-in to more than 64 KB of dynamic LDS
-  if (!attr_set[ropeq]) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, f256::kLds);
-    if (e != hipSuccess) return e;
-    attr_set[ropeq] = true;
-  }
+  static std::atomic<unsigned long long> lds_done[2];  // opt-in to more than 64 KB of dynamic LDS
+  if (const hipError_t e = lds_opt_in(lds_done[ropeq], (const void*)kern, f256::kLds); e != hipSuccess) return e;
   const long blocks = (long)p.b * p.h * p.qblocks * p.nsplit;
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(f256::kThreads), f256::kLds, stream, p);
   return hipGetLastError();

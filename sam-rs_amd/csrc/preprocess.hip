@@ -129,13 +129,11 @@ static hipError_t launch_pre(const unsigned char* img, void* out, int h, int w, 
   const float fx = sx > 1.f ? sx : 1.f, fy = sy > 1.f ? sy : 1.f;
   const int xtaps = preprocess_max_taps(w, nw), ytaps = preprocess_max_taps(h, nh);
   const size_t lds = ((size_t)xtaps * kCols + (size_t)kRows * ytaps + 2 * (kCols + kRows)) * sizeof(float);
-  static bool attr_set = false;  // one-time opt-in to more than the default dynamic LDS
-  if (!attr_set) {
+  static std::atomic<unsigned long long> lds_done{0};  // opt-in to more than the default dynamic LDS
+  {
     const int most = (kMaxTaps * (kCols + kRows) + 2 * (kCols + kRows)) * (int)sizeof(float);
-    hipError_t e = hipFuncSetAttribute((const void*)preprocess_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       most);
+    const hipError_t e = lds_opt_in(lds_done, (const void*)preprocess_kernel<T>, most);
     if (e != hipSuccess) return e;
-    attr_set = true;
   }
   const dim3 grid((unsigned)((size + kCols - 1) / kCols), (unsigned)((size + kRows - 1) / kRows));
   hipLaunchKernelGGL(preprocess_kernel<T>, grid, dim3(kThreads), lds, stream, img, (T*)out, h, w, nh, nw, size, sx, sy,
