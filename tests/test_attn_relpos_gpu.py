@@ -238,3 +238,42 @@ def test_argument_errors_are_reported(hip):
         z = torch.zeros(1, 6, 8, device="cuda", dtype=torch.float64)
         hip.attention_relpos(z, torch.zeros(1, 8, 6, device="cuda", dtype=torch.float64), z,
                              torch.zeros(8, 8, device="cuda", dtype=torch.float64), 2, 3, 0.3)
+
+
+def test_calls_from_two_host_threads(hip):
+    """The C ABI is safe to call from several host threads. Two threads, each on its own stream, run
+    the window kernel (hd 80) and the global kernel (hd 64) twenty times at once. Each final output
+    equals the same call made alone."""
+    import threading
+
+    g = torch.Generator(device="cuda").manual_seed(21)
+    cases = []
+    for h, w, bh, hd in [(14, 14, 50, 80), (64, 64, 2, 64)]:
+        q = torch.randn(bh, h * w, hd, device="cuda", generator=g).half()
+        kt = torch.randn(bh, hd, h * w, device="cuda", generator=g).half()
+        v = torch.randn(bh, h * w, hd, device="cuda", generator=g).half()
+        table = (0.02 * torch.randn(2 * h - 1 + 2 * w - 1, hd, device="cuda", generator=g)).half()
+        args = (q, kt, v, table, h, w, hd ** -0.5)
+        cases.append((args, hip.attention_relpos(*args)))
+    torch.cuda.synchronize()
+    outs, errs = [None, None], []
+
+    def work(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for _ in range(20):
+                    o = hip.attention_relpos(*cases[i][0])
+            s.synchronize()
+            outs[i] = o
+        except Exception as e:  # reported on the main thread
+            errs.append(e)
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads) and not errs, errs
+    for i in range(2):
+        assert torch.equal(outs[i], cases[i][1]), i
