@@ -56,6 +56,10 @@ int check_launch(hipError_t e, const char* what) {
 // The reference's dtype dispatch (kernels.rs:1086-1095) accepts exactly f16, bf16 and f32.
 bool dtype_ok(int dtype) { return dtype == 0 || dtype == 1 || dtype == 2; }
 
+// The kernels move their operands in 16-byte vectors (and by 16-byte LDS DMA), which the header's
+// alignment rule guarantees; a pointer that breaks it is rejected rather than read.
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 }  // namespace
 
 extern "C" {
@@ -76,6 +80,8 @@ int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void
   if (hd % align != 0 || hd > 128)
     return fail(SAM_HIP_EUNSUPPORTED, "attn-relpos: head dim must be a multiple of %d and at most 128, got %d", align,
                 hd);
+  if (!aligned16(q) || !aligned16(kt) || !aligned16(v) || !aligned16(table) || !aligned16(out))
+    return fail(SAM_HIP_EUNSUPPORTED, "attn-relpos: q, kt, v, table and out must be 16-byte aligned");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e = dtype == 0 ? samhip::attn_relpos_f32(q, kt, v, table, out, bh, hd, h, w, scale, s)
                             : samhip::attn_relpos_half(dtype, q, kt, v, table, out, bh, hd, h, w, scale, s);
@@ -101,6 +107,9 @@ int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, vo
     return fail(SAM_HIP_EINVAL, "deform-attn: the levels hold %ld pixels but value has %d", total, s);
   if ((long)b * s * h * d >= (1L << 31))
     return fail(SAM_HIP_EUNSUPPORTED, "deform-attn: value holds more than 2^31 elements");
+  // value rows are gathered and out rows stored in 16-byte vectors; loc and attn are read per element
+  if (!aligned16(value) || !aligned16(out))
+    return fail(SAM_HIP_EUNSUPPORTED, "deform-attn: value and out must be 16-byte aligned");
   hipError_t e = samhip::deform_attn(dtype, value, loc, attn, out, b, s, q, h, d, l, p, shapes,
                                      reinterpret_cast<hipStream_t>(stream));
   return check_launch(e, "deform-attn");
@@ -160,6 +169,8 @@ int sam_hip_relpos_softmax(const void* s, const void* q, const void* table, void
   if (h > 128 || w > 128 || hd > 256)
     return fail(SAM_HIP_EUNSUPPORTED, "relpos-softmax: h, w <= 128 and hd <= 256, got %d, %d, %d", h, w, hd);
   if (rows > 0x7fffffffL) return fail(SAM_HIP_EUNSUPPORTED, "relpos-softmax: more than 2^31 rows");
+  if (!aligned16(s) || !aligned16(q) || !aligned16(table) || !aligned16(out))
+    return fail(SAM_HIP_EUNSUPPORTED, "relpos-softmax: s, q, table and out must be 16-byte aligned");
   hipError_t e = samhip::relpos_softmax(dtype, s, q, table, out, rows, h, w, hd, scale,
                                         reinterpret_cast<hipStream_t>(stream));
   return check_launch(e, "relpos-softmax");
@@ -175,6 +186,8 @@ int sam_hip_qkv_split(const void* y, const void* bias, void* out, int dtype, lon
   if (hd > 256) return fail(SAM_HIP_EUNSUPPORTED, "qkv-split: head dim at most 256, got %d", hd);
   const long blocks = tokens / n * ((n + 63) / 64) * nh;
   if (blocks > 0x7fffffffL) return fail(SAM_HIP_EUNSUPPORTED, "qkv-split: too many tokens");
+  if (!aligned16(y) || !aligned16(bias) || !aligned16(out))
+    return fail(SAM_HIP_EUNSUPPORTED, "qkv-split: y, bias and out must be 16-byte aligned");
   hipError_t e = samhip::qkv_split(dtype, y, bias, out, tokens, n, nh, hd, reinterpret_cast<hipStream_t>(stream));
   return check_launch(e, "qkv-split");
 }
@@ -203,8 +216,6 @@ int get_strides(const long* in, long* out, int l, int h, int d, int elem, const 
       return fail(SAM_HIP_EUNSUPPORTED, "flash-attn: %s strides must be non-negative multiples of 16 bytes", what);
   return SAM_HIP_OK;
 }
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 int device_cus() {
   int dev = 0, cus = 256;

@@ -2,7 +2,8 @@
 
 f32: max|gpu - cpu| / max|cpu| <= 1e-5. f16 / bf16: max-abs <= 2e-3 on attention outputs against the
 f32 oracle run on inputs pre-rounded to the kernel dtype (as tests/kernels.rs:28-31 does); bf16 is
-measured beyond the half-ulp rounding of the bf16 output itself.
+measured beyond the half-ulp rounding of the bf16 output itself, and its raw max-abs is reported beside
+that figure.
 """
 import numpy as np
 import torch
@@ -22,18 +23,30 @@ def bf16_half_ulp(x):
     return 2.0 ** (e - 8)
 
 
+def f16_half_ulp(x):
+    """Half the spacing of f16 numbers at |x| (11 significant bits, subnormal spacing below 2^-14)."""
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -14)))
+    return 2.0 ** (e - 11)
+
+
 def check(got, want, dtype, what):
     """f32: max|gpu-cpu| / max|cpu| <= 1e-5. f16: max-abs <= 2e-3. bf16: max-abs <= 2e-3 beyond the
     half-ulp rounding of the bf16 output itself (|out| >= 0.5 has a half-ulp of 2e-3 or more, so no
-    bf16 result can meet a bare 2e-3 there)."""
+    bf16 result can meet a bare 2e-3 there); the raw max-abs is printed and carried in the message.
+    Returns the figure the bar applies to."""
     assert np.isfinite(got).all(), f"{what}: non-finite output"
+    raw = float(np.abs(got - want).max())
     if dtype == "f32":
-        err = np.abs(got - want).max() / np.abs(want).max()
+        err = raw / float(np.abs(want).max())
+        print(f"parity {what}: max|gpu-cpu|/max|cpu| {err:.3g} (max-abs {raw:.3g})", flush=True)
         assert err <= F32_REL_TOL, f"{what}: max|gpu-cpu|/max|cpu| = {err:.3g}"
     elif dtype == "bf16":
-        err = (np.abs(got - want) - bf16_half_ulp(want)).max()
-        assert err <= HALF_ABS_TOL, f"{what}: max abs diff beyond bf16 output rounding {err:.3g}"
+        err = float((np.abs(got - want) - bf16_half_ulp(want)).max())
+        print(f"parity {what}: raw max-abs {raw:.3g}, beyond bf16 output rounding {err:.3g}", flush=True)
+        assert err <= HALF_ABS_TOL, f"{what}: max abs diff beyond bf16 output rounding {err:.3g} (raw max-abs {raw:.3g})"
     else:
-        err = np.abs(got - want).max()
+        err = raw
+        own = float((np.abs(got - want) - f16_half_ulp(want)).max())
+        print(f"parity {what}: max-abs {raw:.3g} (beyond f16 output rounding {own:.3g})", flush=True)
         assert err <= HALF_ABS_TOL, f"{what}: max abs diff {err:.3g}"
     return err

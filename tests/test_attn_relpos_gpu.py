@@ -44,12 +44,15 @@ def run_gpu(hip, arrays, h, w, scale, dtype):
 # plus small and ragged shapes: a 2x3 grid with hd 8, a single grid row, and odd sizes; 64-column
 # grids with hd 80 and hd 64 of 1, 2, 3, 6 and 37 rows (ring shorter than its depth, odd tile counts, a
 # partial last query block); window grids with hd 80 and hd 64 of 13..16 rows (a full or half-empty
-# last key tile, idle query blocks).
+# last key tile, idle query blocks), and narrow window grids of 2..8 columns, whose 8-slot DMA groups
+# span several grid rows.
 SMALL = [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (2, 3, 2, 8), (1, 5, 2, 16), (5, 33, 2, 32),
          (3, 40, 2, 128), (9, 17, 2, 48), (1, 64, 2, 80), (2, 64, 1, 80), (3, 64, 2, 80), (6, 64, 2, 80),
          (37, 64, 3, 80), (16, 16, 2, 80), (13, 12, 3, 80), (15, 14, 2, 80), (14, 10, 2, 80),
          (1, 64, 2, 64), (2, 64, 1, 64), (3, 64, 2, 64), (37, 64, 3, 64), (16, 16, 2, 64), (13, 12, 3, 64),
-         (15, 14, 2, 64), (14, 10, 2, 64)]
+         (15, 14, 2, 64), (14, 10, 2, 64),
+         (13, 2, 3, 80), (14, 4, 2, 80), (16, 6, 2, 80), (15, 8, 2, 80),
+         (13, 2, 3, 64), (14, 4, 2, 64), (16, 6, 2, 64), (15, 8, 2, 64)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
@@ -62,6 +65,25 @@ def test_attention_relpos_reference_geometries(hip, h, w, bh, hd, dtype):
     want = oracle.attention_relpos(*arrays, h, w, scale)
     got = run_gpu(hip, arrays, h, w, scale, dtype)
     check(got, want, dtype, f"{h}x{w} bh={bh} hd={hd} {dtype}")
+
+
+# The reference test's own draws (tests/kernels.rs:20-37): q, k, v and both tables ~ N(0, 1). Each bias
+# term then has a standard deviation of about sqrt(hd) (8 to 9), so the logits are sharp: a row's
+# softmax is dominated by a few keys and any error in the exp2 argument (the f16 path's pre-scaled q,
+# the bias split into f16 hi / lo halves) shows up undamped. The reference geometries plus the hd-80
+# window and global kernels of ViT-H.
+SHARP = [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (14, 14, 4, 80), (64, 64, 2, 80)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("h,w,bh,hd", SHARP)
+def test_attention_relpos_sharp_logits(hip, h, w, bh, hd, dtype):
+    print(f"attn_relpos sharp {dtype} h={h} w={w} bh={bh} hd={hd}", flush=True)
+    arrays = make_inputs(h, w, bh, hd, 300 + h * w + hd, dtype, qkv_std=1.0, table_std=1.0)
+    scale = hd ** -0.5
+    want = oracle.attention_relpos(*arrays, h, w, scale)
+    got = run_gpu(hip, arrays, h, w, scale, dtype)
+    check(got, want, dtype, f"sharp {h}x{w} bh={bh} hd={hd} {dtype}")
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
@@ -124,26 +146,71 @@ def test_vit_b_l_window_layer(hip, bh, dtype):
     check(got, want, dtype, f"vit-b/l window {dtype} bh={bh}")
 
 
-@pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("bh", [257, 768, 1024, 1600])
-def test_window_kernel_many_units(hip, bh, dtype):
-    """More half units than the 2 x CUs workgroups of the windowed kernel, so workgroups run several
-    in turn through their LDS ring: 257 units (only a few workgroups take a second half unit), 768
-    (three each), 1024 (four), 1600 (ViT-H batch 4: six or seven). The GPU runs every unit; the oracle
-    checks the first and last units, those around each multiple of 256 and a spread in between."""
-    h = w = 14
-    hd = 80
-    print(f"window many units {dtype} bh={bh}", flush=True)
-    arrays = make_inputs(h, w, bh, hd, 50 + bh, dtype)
-    scale = hd ** -0.5
-    got = run_gpu(hip, arrays, h, w, scale, dtype)
-    units = set(np.linspace(0, bh - 1, 16).astype(int).tolist())
-    for m in range(0, bh + 1, 256):
+def device_inputs(h, w, bh, hd, seed, dtype, table_std=0.02):
+    """q, k, v ~ N(0,1) and a table ~ N(0, table_std), drawn on the device in the kernel dtype (the
+    large launches would take long to draw and move on the host)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    dt = TORCH_DT[dtype]
+    n = h * w
+    q = torch.randn(bh, n, hd, device="cuda", generator=g).to(dt)
+    kt = torch.randn(bh, hd, n, device="cuda", generator=g).to(dt)
+    v = torch.randn(bh, n, hd, device="cuda", generator=g).to(dt)
+    table = (table_std * torch.randn(2 * h - 1 + 2 * w - 1, hd, device="cuda", generator=g)).to(dt)
+    return q, kt, v, table
+
+
+def sampled_units(bh, period):
+    """The first and last units, those around every multiple of `period` and a spread in between."""
+    units = set(np.linspace(0, bh - 1, 12).astype(int).tolist())
+    for m in range(0, bh + 1, period):
         units.update(u for u in (m - 1, m, m + 1) if 0 <= u < bh)
-    units = sorted(units)
-    q, kt, v, table = arrays
-    want = oracle.attention_relpos(q[units], kt[units], v[units], table, h, w, scale)
-    check(got[units], want, dtype, f"window kernel bh={bh} {dtype}")
+    return sorted(units)
+
+
+def check_units(hip, tensors, units, h, w, dtype, what):
+    q, kt, v, table = tensors
+    hd = q.shape[2]
+    got = hip.attention_relpos(q, kt, v, table, h, w, hd ** -0.5)
+    torch.cuda.synchronize()
+    idx = torch.tensor(units, device="cuda")
+    host = lambda t: t.float().cpu().numpy()
+    want = oracle.attention_relpos(host(q[idx]), host(kt[idx]), host(v[idx]), host(table), h, w, hd ** -0.5)
+    check(host(got[idx]), want, dtype, what)
+
+
+# Window launches with more half-unit workgroups than the chip holds at once (two per CU at hd 80,
+# three at hd 64), so the hardware schedules them in several rounds: 257 units (a few workgroups in a
+# second round), 768 and 1024 at hd 80, and the encoder sweep's batch 4 and 8: ViT-B 1200 and 2400
+# units, ViT-L 1600 and 3200 (hd 64), ViT-H 1600 and 3200 (hd 80).
+MANY_UNITS = [(80, 257), (80, 768), (80, 1024), (80, 1600), (80, 3200), (64, 1200), (64, 1600), (64, 2400),
+              (64, 3200)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("hd,bh", MANY_UNITS)
+def test_window_kernel_many_units(hip, hd, bh, dtype):
+    """Every unit runs on the GPU; the oracle checks the first and last units, those around each
+    multiple of 256 and a spread in between."""
+    h = w = 14
+    print(f"window many units {dtype} hd={hd} bh={bh}", flush=True)
+    tensors = device_inputs(h, w, bh, hd, 50 + bh + hd, dtype)
+    check_units(hip, tensors, sampled_units(bh, 256), h, w, dtype, f"window kernel hd={hd} bh={bh} {dtype}")
+
+
+# Global launches of the encoder sweep beyond one head block per CU: ViT-B batch 4 and 8 (48, 96
+# heads), ViT-L batch 4 and 8 (64, 128) at hd 64, ViT-H batch 4 (64) at hd 80. The oracle checks the
+# first and last heads and a few between.
+MANY_HEADS = [(64, 48), (64, 64), (64, 96), (64, 128), (80, 64)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("hd,bh", MANY_HEADS)
+def test_global_kernel_many_heads(hip, hd, bh, dtype):
+    h = w = 64
+    print(f"global many heads {dtype} hd={hd} bh={bh}", flush=True)
+    tensors = device_inputs(h, w, bh, hd, 70 + bh + hd, dtype)
+    heads = sorted({0, 1, bh // 2, bh - 2, bh - 1})
+    check_units(hip, tensors, heads, h, w, dtype, f"global kernel hd={hd} bh={bh} {dtype}")
 
 
 def test_window_kernel_units_are_independent(hip):
@@ -240,40 +307,79 @@ def test_argument_errors_are_reported(hip):
                              torch.zeros(8, 8, device="cuda", dtype=torch.float64), 2, 3, 0.3)
 
 
-def test_calls_from_two_host_threads(hip):
-    """The C ABI is safe to call from several host threads. Two threads, each on its own stream, run
-    the window kernel (hd 80) and the global kernel (hd 64) twenty times at once. Each final output
-    equals the same call made alone."""
-    import threading
+def test_misaligned_operands_are_rejected(hip):
+    """The kernels move q, kT, v, the table and out in 16-byte vectors, so the C ABI rejects pointers
+    that are not 16-byte aligned instead of running on them. A view that starts one element into a
+    buffer is contiguous but misaligned."""
+    h = w = 14
+    bh, hd = 2, 64
+    n = h * w
+    buf = torch.zeros(bh * n * hd + 8, device="cuda", dtype=torch.float16)
+    ok = buf[: bh * n * hd].view(bh, n, hd)
+    bad = buf[1: 1 + bh * n * hd].view(bh, n, hd)
+    kt = torch.zeros(bh, hd, n, device="cuda", dtype=torch.float16)
+    t = torch.zeros(2 * h - 1 + 2 * w - 1, hd, device="cuda", dtype=torch.float16)
+    hip.attention_relpos(ok, kt, ok, t, h, w, 0.125)
+    for args in [(bad, kt, ok, t), (ok, kt, bad, t)]:
+        with pytest.raises(hip.SamHipError, match="16-byte aligned"):
+            hip.attention_relpos(*args, h, w, 0.125)
 
-    g = torch.Generator(device="cuda").manual_seed(21)
-    cases = []
-    for h, w, bh, hd in [(14, 14, 50, 80), (64, 64, 2, 64)]:
-        q = torch.randn(bh, h * w, hd, device="cuda", generator=g).half()
-        kt = torch.randn(bh, hd, h * w, device="cuda", generator=g).half()
-        v = torch.randn(bh, h * w, hd, device="cuda", generator=g).half()
-        table = (0.02 * torch.randn(2 * h - 1 + 2 * w - 1, hd, device="cuda", generator=g)).half()
-        args = (q, kt, v, table, h, w, hd ** -0.5)
-        cases.append((args, hip.attention_relpos(*args)))
+
+_THREADS_CHILD = r"""
+import sys, threading
+sys.path.insert(0, sys.argv[1])
+import torch
+import sam_hip
+sam_hip.load()
+g = torch.Generator(device="cuda").manual_seed(21)
+cases = []
+for h, w, bh, hd in [(14, 14, 50, 80), (64, 64, 2, 64), (64, 64, 2, 80), (14, 14, 30, 64)]:
+    q = torch.randn(bh, h * w, hd, device="cuda", generator=g).half()
+    kt = torch.randn(bh, hd, h * w, device="cuda", generator=g).half()
+    v = torch.randn(bh, h * w, hd, device="cuda", generator=g).half()
+    table = (0.02 * torch.randn(2 * h - 1 + 2 * w - 1, hd, device="cuda", generator=g)).half()
+    cases.append((q, kt, v, table, h, w, hd ** -0.5))
+torch.cuda.synchronize()
+outs, errs = {}, []
+start = threading.Barrier(2)
+
+def work(i):
+    try:
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            start.wait()
+            # both threads make the first call of every kernel instance at about the same time
+            order = range(len(cases)) if i == 0 else reversed(range(len(cases)))
+            for _ in range(10):
+                for c in order:
+                    outs[(i, c)] = sam_hip.attention_relpos(*cases[c])
+        s.synchronize()
+    except Exception as e:
+        errs.append(repr(e))
+
+threads = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+for t in threads: t.start()
+for t in threads: t.join(timeout=60)
+assert not any(t.is_alive() for t in threads), "a thread did not finish"
+assert not errs, errs
+for c in range(len(cases)):
+    ref = sam_hip.attention_relpos(*cases[c])
     torch.cuda.synchronize()
-    outs, errs = [None, None], []
-
-    def work(i):
-        try:
-            s = torch.cuda.Stream()
-            with torch.cuda.stream(s):
-                for _ in range(20):
-                    o = hip.attention_relpos(*cases[i][0])
-            s.synchronize()
-            outs[i] = o
-        except Exception as e:  # reported on the main thread
-            errs.append(e)
-
-    threads = [threading.Thread(target=work, args=(i,)) for i in range(2)]
-    for t in threads:
-        t.start()
-    for t in threads:
-        t.join(timeout=60)
-    assert not any(t.is_alive() for t in threads) and not errs, errs
     for i in range(2):
-        assert torch.equal(outs[i], cases[i][1]), i
+        assert torch.equal(outs[(i, c)], ref), (i, c)
+print("threads ok", flush=True)
+"""
+
+
+def test_calls_from_two_host_threads(hip):
+    """The C ABI is safe to call from several host threads, including the first call of each kernel
+    (its once-per-device LDS opt-in). A fresh child process, whose first calls into the library come
+    from two threads on their own streams at once, runs the window and global kernels at hd 64 and 80
+    ten times each; every output equals the same call made afterwards from the main thread."""
+    import os
+    import subprocess
+    import sys
+
+    pkg = os.path.dirname(hip.__file__)
+    r = subprocess.run([sys.executable, "-c", _THREADS_CHILD, pkg], capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and "threads ok" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
