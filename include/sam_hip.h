@@ -10,8 +10,9 @@
  *   - stream: a hipStream_t passed as void* (NULL = the default stream); launches are asynchronous,
  *     exactly as the reference's are on candle's CUDA stream;
  *   - return 0 on success, nonzero on error; sam_hip_last_error() then returns a message (per thread);
- *   - no global mutable state beyond each kernel's once-per-device LDS opt-in (an atomic flag word);
- *     safe to call from many threads.
+ *   - no global mutable state beyond each kernel's once-per-device LDS opt-in (an atomic flag word)
+ *     and the workspace array of sam_hip_flash_attn_noalloc; safe to call from many threads (except
+ *     that overlapping sam_hip_flash_attn_noalloc calls on one GPU share that array).
  */
 #ifndef SAM_HIP_H
 #define SAM_HIP_H
@@ -134,6 +135,23 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
                        const long* strides_o, float scale, const float* rope_cos, const float* rope_sin,
                        int rope_rows, int n_rope_q, int n_rope_k, void* workspace, long workspace_bytes,
                        void* stream);
+
+/*
+ * sam_hip_flash_attn without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart
+ * in the reference: its GPU flash attention allocates internally. The workspace comes from a fixed
+ * array of SAM_HIP_FLASH_NOALLOC_MAX_BYTES bytes that the library holds on every GPU it runs on until
+ * the process ends; a call whose sam_hip_flash_attn_workspace_size exceeds it fails with
+ * SAM_HIP_EUNSUPPORTED (SAM 2.1 memory attention needs about 51 MB). The call itself allocates
+ * nothing. All calls on one GPU share that array: calls on one stream are ordered and safe, calls that
+ * overlap on one GPU (several streams or threads) race. Arguments and limits otherwise as
+ * sam_hip_flash_attn.
+ */
+#define SAM_HIP_FLASH_NOALLOC_MAX_BYTES (64L << 20)
+int sam_hip_flash_attn_noalloc(const void* q, const void* k, const void* v, void* out, int dtype, int b, int lq,
+                               int lk, int h, int d, const long* strides_q, const long* strides_k,
+                               const long* strides_v, const long* strides_o, float scale, const float* rope_cos,
+                               const float* rope_sin, int rope_rows, int n_rope_q, int n_rope_k, void* stream);
 
 /*
  * 2-D axial RoPE on rows of a [b, l, h, d] tensor (strides as for flash attention, NULL = contiguous):

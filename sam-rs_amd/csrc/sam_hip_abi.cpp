@@ -62,9 +62,17 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
+namespace samhip {
+// Sets this thread's sam_hip_last_error message (for entry points defined in other files).
+int report_error(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+}  // namespace samhip
+
 extern "C" {
 
-int sam_hip_abi_version(void) { return 2; }
+int sam_hip_abi_version(void) { return 3; }
 
 const char* sam_hip_last_error(void) { return g_last_error.c_str(); }
 

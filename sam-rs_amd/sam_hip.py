@@ -66,6 +66,8 @@ def load():
         L.sam_hip_flash_attn.argtypes = [_vp] * 4 + [_i] * 6 + [_lp] * 4 + [_f, _vp, _vp, _i, _i, _i, _vp,
                                                                         ctypes.c_long, _vp]
         L.sam_hip_flash_attn.restype = _i
+        L.sam_hip_flash_attn_noalloc.argtypes = [_vp] * 4 + [_i] * 6 + [_lp] * 4 + [_f, _vp, _vp, _i, _i, _i, _vp]
+        L.sam_hip_flash_attn_noalloc.restype = _i
         L.sam_hip_rope.argtypes = [_vp] * 4 + [_i] * 5 + [_lp] * 2 + [_i, _i, _vp]
         L.sam_hip_rope.restype = _i
         _lib = L
@@ -272,7 +274,8 @@ def _strides_blhd(t: torch.Tensor, layout: str):
     return (ctypes.c_long * 3)(*s)
 
 
-def _flash(q, k, v, out, layout: str, scale: float, cos=None, sin=None, n_rope_q: int = 0, n_rope_k: int = 0):
+def _flash(q, k, v, out, layout: str, scale: float, cos=None, sin=None, n_rope_q: int = 0, n_rope_k: int = 0,
+           noalloc: bool = False):
     for t in (q, k, v):
         if not t.is_cuda:
             raise SamHipError("sam-rs HIP kernels need device tensors")
@@ -288,28 +291,40 @@ def _flash(q, k, v, out, layout: str, scale: float, cos=None, sin=None, n_rope_q
     if (kb, kh, kd) != (b, h, d):  # kernels.rs:425-427
         raise SamHipError(f"flash-attn: incompatible q/k/v shapes {tuple(q.shape)}/{tuple(k.shape)}/{tuple(v.shape)}")
     L = load()
+    cs = cos.data_ptr() if cos is not None else None
+    sn = sin.data_ptr() if sin is not None else None
+    rows = cos.shape[0] if cos is not None else 0
+    if noalloc:
+        # the library's own workspace array: no device allocation for this call
+        _check(L.sam_hip_flash_attn_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dt, b, lq, lk,
+                                            h, d, _strides_blhd(q, layout), _strides_blhd(k, layout),
+                                            _strides_blhd(v, layout), _strides_blhd(out, layout), scale, cs, sn, rows,
+                                            n_rope_q, n_rope_k, _stream()))
+        return out
     ws_bytes = L.sam_hip_flash_attn_workspace_size(dt, b, lq, lk, h, d, n_rope_k)
     if ws_bytes < 0:
         raise SamHipError(L.sam_hip_last_error().decode())
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     rc = L.sam_hip_flash_attn(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dt, b, lq, lk, h, d,
                               _strides_blhd(q, layout), _strides_blhd(k, layout), _strides_blhd(v, layout),
-                              _strides_blhd(out, layout), scale,
-                              cos.data_ptr() if cos is not None else None, sin.data_ptr() if sin is not None else None,
-                              cos.shape[0] if cos is not None else 0, n_rope_q, n_rope_k, ws.data_ptr(), ws_bytes,
-                              _stream())
+                              _strides_blhd(out, layout), scale, cs, sn, rows, n_rope_q, n_rope_k, ws.data_ptr(),
+                              ws_bytes, _stream())
     _check(rc)
     return out
 
 
-def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None) -> torch.Tensor:
+def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None,
+               out: torch.Tensor | None = None, noalloc: bool = False) -> torch.Tensor:
     """softmax(scale * q k^T) v without a mask on q [B, Lq, H, D], k/v [B, Lk, H, D] -> [B, Lq, H, D]
     (f16 / bf16), as candle_flash_attn::flash_attn(q, k, v, scale, false) and kernels::flash_attn_cpu
-    compute it. scale defaults to D^-0.5, the value every reference caller passes."""
+    compute it. scale defaults to D^-0.5, the value every reference caller passes. With noalloc the call
+    goes through sam_hip_flash_attn_noalloc (the library's fixed workspace array; no allocation when
+    `out` is given)."""
     d = q.shape[-1]
     scale = float(d) ** -0.5 if scale is None else float(scale)
-    out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    return _flash(q, k, v, out, "blhd", scale)
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    return _flash(q, k, v, out, "blhd", scale, noalloc=noalloc)
 
 
 def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask=None) -> torch.Tensor:
@@ -350,7 +365,7 @@ def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_rot: int | Non
 
 
 def rope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-                   n_exclude: int) -> torch.Tensor:
+                   n_exclude: int, noalloc: bool = False) -> torch.Tensor:
     """The attention core of RopeAttn::forward (sam3/video.rs:129-145) after the projections, one head:
     q [B, Lq, D] rotated with the tables, the first M - n_exclude keys of k [B, M, D] rotated with the
     tables tiled to their length, the last n_exclude (object pointers) not, then sdpa with v [B, M, D].
@@ -368,5 +383,5 @@ def rope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch
         raise SamHipError(f"rope_attention: {lq} queries but the tables have {cos.shape[0]} rows")
     out = torch.empty((b, lq, d), dtype=q.dtype, device=q.device)
     _flash(q.unsqueeze(2), k.unsqueeze(2), v.unsqueeze(2), out.unsqueeze(2), "blhd", float(d) ** -0.5, cos, sin,
-           lq, rot)
+           lq, rot, noalloc=noalloc)
     return out

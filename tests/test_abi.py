@@ -27,7 +27,7 @@ def lib():
 def test_header_declares_the_entry_points():
     names = declared_functions()
     for want in ("sam_hip_attn_relpos", "sam_hip_relpos_softmax", "sam_hip_qkv_split", "sam_hip_deform_attn",
-                 "sam_hip_flash_attn", "sam_hip_flash_attn_workspace_size", "sam_hip_rope", "sam_hip_last_error",
+                 "sam_hip_flash_attn", "sam_hip_flash_attn_workspace_size", "sam_hip_flash_attn_noalloc", "sam_hip_rope", "sam_hip_last_error",
                  "sam_hip_abi_version"):
         assert want in names
 
