@@ -78,6 +78,21 @@ int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, vo
                         int q, int h, int d, int l, int p, const int* shapes, void* stream);
 
 /*
+ * Grounding DINO's Deform::forward between its input projections and its output projection
+ * (dino/mod.rs:161-181 without the four Linear layers), in one launch:
+ *   attn = softmax over the l*p points of each (b, q, h) of logits [b, q, h, l, p]          (:167)
+ *   loc  = refs[b,q,l,0:2] + offsets / (W_l, H_l)                       ncoord 2, encoder (:169-173)
+ *   loc  = refs[b,q,l,0:2] + ((offsets * (1/p)) * refs[b,q,l,2:4]) * 0.5  ncoord 4, decoder (:174-178)
+ *   out  = deform_attn(value, loc, attn, shapes)                                             (:179)
+ * with offsets [b, q, h, l, p, 2] (the sampling_offsets projection reshaped), refs [b, q, l, ncoord].
+ * loc and attn are formed per point in f32 and never stored. Limits and alignment as
+ * sam_hip_deform_attn; ncoord is 2 or 4.
+ */
+int sam_hip_deform_core(const void* value, const void* offsets, const void* logits, const void* refs, void* out,
+                        int dtype, int b, int s, int q, int h, int d, int l, int p, int ncoord, const int* shapes,
+                        void* stream);
+
+/*
  * SAM image preprocessing: antialiased triangle-filter resize (PIL's bilinear) of an RGB u8 image
  * img [h, w, 3] to nh x nw, then (x - mean[c]) / std_dev[c], zero padded at the bottom and right into
  * out [3, size, size] of `dtype`. mean and std_dev are host arrays of 3 floats.

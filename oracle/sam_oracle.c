@@ -199,6 +199,42 @@ static void softmax_div(float* x, int n) {
   for (int k = 0; k < n; ++k) x[k] = x[k] / sum;
 }
 
+/* Deform::forward between its input projections and deform_attn (dino/mod.rs:166-178):
+ *   attn = softmax over the l*p points of each (b, q, h) of the logits [b,q,h,l,p] (:167);
+ *   loc from the offsets off [b,q,h,l,p,2] and the reference points refs [b,q,l,ncoord]:
+ *     ncoord 2 (encoder, :169-173): loc = ref + off / (W_l, H_l);
+ *     ncoord 4 (decoder, :174-178): loc = xy + ((off * (1/p)) * wh) * 0.5, where candle's `off / p`
+ *       is Tensor::affine(1/p, 0) (x * mul + add) and `.affine(0.5, 0.0)` is x * 0.5 + 0.
+ * Every step is one f32 rounding, left to right, as the candle ops compute them. */
+void oracle_deform_prep(const float* off, const float* logits, const float* refs, float* loc, float* attn, int b,
+                        int q, int h, int l, int p, int ncoord, const int* shapes, int nthreads) {
+  const long pairs = (long)b * q * h;
+  const int npt = l * p;
+  const float inv_p = (float)(1.0 / (double)p);
+#pragma omp parallel for schedule(static) num_threads(threads_or_all(nthreads))
+  for (long pr = 0; pr < pairs; ++pr) {
+    const long bq = pr / h;
+    float* a = attn + pr * npt;
+    for (int j = 0; j < npt; ++j) a[j] = logits[pr * npt + j];
+    softmax_div(a, npt);
+    for (int j = 0; j < npt; ++j) {
+      const int li = j / p;
+      const float* r = refs + (bq * l + li) * ncoord;
+      const float ox = off[(pr * npt + j) * 2], oy = off[(pr * npt + j) * 2 + 1];
+      float* o = loc + (pr * npt + j) * 2;
+      if (ncoord == 2) {
+        o[0] = r[0] + ox / (float)shapes[2 * li + 1];
+        o[1] = r[1] + oy / (float)shapes[2 * li];
+      } else {
+        const float tx = ox * inv_p + 0.0f, ty = oy * inv_p + 0.0f;
+        const float ux = tx * r[2], uy = ty * r[3];
+        o[0] = r[0] + (ux * 0.5f + 0.0f);
+        o[1] = r[1] + (uy * 0.5f + 0.0f);
+      }
+    }
+  }
+}
+
 void oracle_sdpa(const float* q, const float* k, const float* v, float* out, int b, int h, int lq, int lk, int d,
                  int nthreads) {
   const float scale = powf((float)d, -0.5f);

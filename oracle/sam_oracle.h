@@ -40,6 +40,12 @@ void oracle_qkv_split(const float* y, const float* bias, float* out, long tokens
 void oracle_deform_attn(const float* value, const float* loc, const float* attn, float* out, int b, int s, int q, int h,
                         int d, int l, int p, const int* shapes, int nthreads);
 
+/* dino/mod.rs:166-178 (Deform::forward after its input projections): softmax of logits [b,q,h,l,p]
+ * over l*p -> attn; offsets off [b,q,h,l,p,2] and refs [b,q,l,ncoord] (ncoord 2: encoder, 4: decoder)
+ * -> loc [b,q,h,l,p,2]; shapes = l (height,width) pairs. */
+void oracle_deform_prep(const float* off, const float* logits, const float* refs, float* loc, float* attn, int b,
+                        int q, int h, int l, int p, int ncoord, const int* shapes, int nthreads);
+
 /* sam3/nn.rs:26-34 (sdpa, mask = None) on [b, h, l, d] tensors: softmax(q k^T * d^-0.5) v. */
 void oracle_sdpa(const float* q, const float* k, const float* v, float* out, int b, int h, int lq, int lk, int d,
                  int nthreads);

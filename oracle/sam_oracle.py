@@ -42,6 +42,7 @@ def lib():
         L.oracle_qkv_split.argtypes = [_F, _F, _F, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_int]
         L.oracle_deform_attn.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 7 + [_I, ctypes.c_int]
+        L.oracle_deform_prep.argtypes = [_F] * 5 + [ctypes.c_int] * 6 + [_I, ctypes.c_int]
         L.oracle_sdpa.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 6
         L.oracle_mha_blhd.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int]
         L.oracle_rope_tables.argtypes = [ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_float, _F, _F]
@@ -109,6 +110,27 @@ def deform_attn(value, loc, attn, shapes, nthreads: int = 0) -> np.ndarray:
     lib().oracle_deform_attn(_p(value), _p(loc), _p(attn), _p(out), b, s, q, h, d, l, p, sh.ctypes.data_as(_I),
                              nthreads)
     return out
+
+
+def deform_prep(off, logits, refs, shapes, nthreads: int = 0):
+    """dino/mod.rs:166-178. off [B,Q,H,L,P,2], logits [B,Q,H,L,P], refs [B,Q,L,2|4] -> (loc, attn)."""
+    off, logits, refs = _f32(off), _f32(logits), _f32(refs)
+    b, q, h, l, p, two = off.shape
+    nc = refs.shape[-1]
+    assert two == 2 and logits.shape == (b, q, h, l, p) and refs.shape == (b, q, l, nc) and nc in (2, 4)
+    assert len(shapes) == l
+    sh = np.ascontiguousarray(np.array(shapes, np.int32).reshape(-1))
+    loc = np.empty_like(off)
+    attn = np.empty_like(logits)
+    lib().oracle_deform_prep(_p(off), _p(logits), _p(refs), _p(loc), _p(attn), b, q, h, l, p, nc,
+                             sh.ctypes.data_as(_I), nthreads)
+    return loc, attn
+
+
+def deform_forward_core(value, off, logits, refs, shapes, nthreads: int = 0) -> np.ndarray:
+    """Deform::forward between its projections (dino/mod.rs:166-179): deform_prep, then deform_attn."""
+    loc, attn = deform_prep(off, logits, refs, shapes, nthreads)
+    return deform_attn(value, loc, attn, shapes, nthreads)
 
 
 def sdpa(q, k, v, nthreads: int = 0) -> np.ndarray:

@@ -20,6 +20,12 @@
 //   [B, S, H, D]: a head's row of a pixel is its own D-element run, shared with no other head).
 // - deform_attn_kernel (other D, or more than 3.75 GB of value): the same contract with scalar lanes
 //   and a branch per corner.
+//
+// Both kernels also take the inputs of Deform::forward between its projections (dino/mod.rs:166-178)
+// in place of loc and attn (template parameter NC = 2 or 4): the sampling offsets [B,Q,H,L,P,2], the
+// attention logits [B,Q,H,L,P] and the reference points [B,Q,L,NC]. The pair's lanes then softmax its
+// L*P logits and form each point's location while they build its corner table, so the locations and
+// weights never go through memory (the reference writes and reads both as tensors).
 #include "common.hpp"
 
 namespace samhip {
@@ -39,10 +45,62 @@ template <> struct VecLoad<f16, 8> { typedef f16x8 type; };
 template <> struct VecLoad<bf16, 8> { typedef bf16x8 type; };
 template <typename T> struct VecLoad<T, 1> { typedef T type; };
 
-template <typename T, int VEC>
-__global__ __launch_bounds__(kDeformThreads) void deform_attn_kernel(const T* __restrict__ value,
-                                                                    const T* __restrict__ loc,
-                                                                    const T* __restrict__ attn,
+// Where a pair's points come from. NC = 0: loc and attn as the reference's deform_attn takes them.
+// NC = 2 or 4: loc holds the sampling offsets, attn the attention logits, refs the reference points.
+template <typename T> struct PointSrc {
+  const T* loc;
+  const T* attn;
+  const T* refs;
+  float inv_p;  // (float)(1 / P): candle's `off / p` is affine(1/p, 0)
+};
+
+// Softmax statistics of a pair's L*P logits (NC != 0): their max and the sum of exp(x - max), reduced
+// over the LP lanes li = 0..LP-1 of the pair's lane group. Every lane of the wave takes part.
+template <typename T>
+__device__ __forceinline__ void pair_softmax(const T* logits, long base0, int npt, int li, int LP, bool valid,
+                                             float& mx, float& sum) {
+  float m = -INFINITY;
+  if (valid)
+    for (int j = li; j < npt; j += LP) m = fmaxf(m, to_f32(logits[base0 + j]));
+  for (int o = LP >> 1; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  float s = 0.f;
+  if (valid)
+    for (int j = li; j < npt; j += LP) s += expf(to_f32(logits[base0 + j]) - m);
+  for (int o = LP >> 1; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  mx = m;
+  sum = s;
+}
+
+// Point j (level l) of pair `pair` (bq = b * Q + q): normalised location (x, y) and weight w.
+// NC = 2 (encoder, dino/mod.rs:169-173): loc = ref + off / (W_l, H_l).
+// NC = 4 (decoder, dino/mod.rs:174-178): loc = xy + ((off * (1/P)) * wh) * 0.5.
+// Each step is one f32 rounding, as the reference's tensor ops are (no contraction).
+template <typename T, int NC>
+__device__ __forceinline__ void point_xyw(const PointSrc<T>& src, long pair, long bq, int npt, int j, int l, int L,
+                                          int Wl, int Hl, float mx, float sum, float& x, float& y, float& w) {
+#pragma clang fp contract(off)
+  const long base = pair * npt + j;
+  const float ax = to_f32(src.loc[base * 2]), ay = to_f32(src.loc[base * 2 + 1]);
+  if constexpr (NC == 0) {
+    w = to_f32(src.attn[base]);
+    x = ax;
+    y = ay;
+  } else {
+    w = expf(to_f32(src.attn[base]) - mx) / sum;
+    const T* r = src.refs + (bq * L + l) * NC;
+    if constexpr (NC == 2) {
+      x = to_f32(r[0]) + ax / (float)Wl;
+      y = to_f32(r[1]) + ay / (float)Hl;
+    } else {
+      const float ux = (ax * src.inv_p) * to_f32(r[2]), uy = (ay * src.inv_p) * to_f32(r[3]);
+      x = to_f32(r[0]) + ux * 0.5f;
+      y = to_f32(r[1]) + uy * 0.5f;
+    }
+  }
+}
+
+template <typename T, int VEC, int NC>
+__global__ __launch_bounds__(kDeformThreads) void deform_attn_kernel(const T* __restrict__ value, PointSrc<T> src,
                                                                     T* __restrict__ out, int B, int S, int Q,
                                                                     int H, int D, int L, int P, int lp_shift,
                                                                     Levels lv) {
@@ -62,15 +120,18 @@ __global__ __launch_bounds__(kDeformThreads) void deform_attn_kernel(const T* __
   const int h = valid ? (int)(pair % H) : 0;
   const long bq = valid ? pair / H : 0;  // b * Q + q
   const long b = bq / Q;
+  float mx = 0.f, sum = 1.f;
+  if constexpr (NC != 0) pair_softmax(src.attn, pair * npt, npt, li, LP, valid, mx, sum);
   for (int j = li; j < npt; j += LP) {
     const int l = j / P;
     int2 c4[4];
     if (valid) {
-      const long base = pair * npt + j;  // ((b*Q + q)*H + h)*L*P + l*P + p
-      const float wgt = to_f32(attn[base]);
+      // point ((b*Q + q)*H + h)*L*P + l*P + p
       const int Hl = lv.h[l], Wl = lv.w[l];
-      const float x = to_f32(loc[base * 2]) * (float)Wl - 0.5f;
-      const float y = to_f32(loc[base * 2 + 1]) * (float)Hl - 0.5f;
+      float lx, ly, wgt;
+      point_xyw<T, NC>(src, pair, bq, npt, j, l, L, Wl, Hl, mx, sum, lx, ly, wgt);
+      const float x = lx * (float)Wl - 0.5f;
+      const float y = ly * (float)Hl - 0.5f;
       const float xf = floorf(x), yf = floorf(y);
       const int x0 = (int)xf, y0 = (int)yf;
       const float fx = x - xf, fy = y - yf;
@@ -130,10 +191,9 @@ __global__ __launch_bounds__(kDeformThreads) void deform_attn_kernel(const T* __
 constexpr int kDeformUnroll = 16;
 constexpr unsigned kDeformSkip = 0xF0000000u;
 
-template <typename T, int VEC>
+template <typename T, int VEC, int NC>
 __global__ __launch_bounds__(kDeformThreads) void deform_attn_gather_kernel(const T* __restrict__ value,
-                                                                           const T* __restrict__ loc,
-                                                                           const T* __restrict__ attn,
+                                                                           PointSrc<T> src,
                                                                            T* __restrict__ out, int B, int S,
                                                                            int Q, int H, int D, int L, int P,
                                                                            int lp_shift, int ntab, Levels lv) {
@@ -158,17 +218,20 @@ __global__ __launch_bounds__(kDeformThreads) void deform_attn_gather_kernel(cons
   const long pair = bq * H + h;  // index of the (b, q, h) pair in loc and attn
   // corner table of this pair: ntab entries of (byte offset into value, weight)
   int2* corners = reinterpret_cast<int2*>(smem) + ((long)wave * ppw + sub) * ntab;
+  float mx = 0.f, sum = 1.f;
+  if constexpr (NC != 0) pair_softmax(src.attn, pair * npt, npt, li, LP, valid, mx, sum);
   for (int j = li; j < (ntab >> 2); j += LP) {
     int2 c4[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) c4[c] = make_int2((int)kDeformSkip, 0);
     if (valid && j < npt) {
       const int l = j / P;
-      const long base = pair * npt + j;  // ((b*Q + q)*H + h)*L*P + l*P + p
-      const float wgt = to_f32(attn[base]);
+      // point ((b*Q + q)*H + h)*L*P + l*P + p
       const int Hl = lv.h[l], Wl = lv.w[l];
-      const float x = to_f32(loc[base * 2]) * (float)Wl - 0.5f;
-      const float y = to_f32(loc[base * 2 + 1]) * (float)Hl - 0.5f;
+      float lx, ly, wgt;
+      point_xyw<T, NC>(src, pair, bq, npt, j, l, L, Wl, Hl, mx, sum, lx, ly, wgt);
+      const float x = lx * (float)Wl - 0.5f;
+      const float y = ly * (float)Hl - 0.5f;
       const float xf = floorf(x), yf = floorf(y);
       const int x0 = (int)xf, y0 = (int)yf;
       const float fx = x - xf, fy = y - yf;
@@ -217,9 +280,9 @@ __global__ __launch_bounds__(kDeformThreads) void deform_attn_gather_kernel(cons
   }
 }
 
-template <typename T, int VEC>
-static hipError_t launch_deform(const void* value, const void* loc, const void* attn, void* out, int b, int s, int q,
-                                int h, int d, int l, int p, const Levels& lv, hipStream_t stream) {
+template <typename T, int VEC, int NC>
+static hipError_t launch_deform(const void* value, PointSrc<T> src, void* out, int b, int s, int q, int h, int d, int l,
+                                int p, const Levels& lv, hipStream_t stream) {
   // at least 8 lanes per pair keeps the corner tables within 64 KB of LDS (8 pairs x 64 points per wave)
   const int lanes = (d + VEC - 1) / VEC;
   int shift = 3;
@@ -229,14 +292,14 @@ static hipError_t launch_deform(const void* value, const void* loc, const void* 
   const long waves = (pairs + ppw - 1) / ppw;
   const long blocks = (waves + kDeformThreads / 64 - 1) / (kDeformThreads / 64);
   const size_t lds = (size_t)(kDeformThreads / 64) * ppw * l * p * 4 * sizeof(int2);
-  hipLaunchKernelGGL((deform_attn_kernel<T, VEC>), dim3((unsigned)blocks), dim3(kDeformThreads), lds, stream,
-                     (const T*)value, (const T*)loc, (const T*)attn, (T*)out, b, s, q, h, d, l, p, shift, lv);
+  hipLaunchKernelGGL((deform_attn_kernel<T, VEC, NC>), dim3((unsigned)blocks), dim3(kDeformThreads), lds, stream,
+                     (const T*)value, src, (T*)out, b, s, q, h, d, l, p, shift, lv);
   return hipGetLastError();
 }
 
-template <typename T, int VEC>
-static hipError_t launch_gather(const void* value, const void* loc, const void* attn, void* out, int b, int s, int q,
-                                int h, int d, int l, int p, const Levels& lv, hipStream_t stream) {
+template <typename T, int VEC, int NC>
+static hipError_t launch_gather(const void* value, PointSrc<T> src, void* out, int b, int s, int q, int h, int d, int l,
+                                int p, const Levels& lv, hipStream_t stream) {
   const int lanes = d / VEC;
   int shift = 3;
   while ((1 << shift) < lanes && shift < 6) ++shift;
@@ -246,25 +309,23 @@ static hipError_t launch_gather(const void* value, const void* loc, const void* 
   const long waves = (pairs + ppw - 1) / ppw;
   const long blocks = (waves + kDeformThreads / 64 - 1) / (kDeformThreads / 64);
   const size_t lds = (size_t)(kDeformThreads / 64) * ppw * ntab * sizeof(int2);
-  hipLaunchKernelGGL((deform_attn_gather_kernel<T, VEC>), dim3((unsigned)blocks), dim3(kDeformThreads), lds, stream,
-                     (const T*)value, (const T*)loc, (const T*)attn, (T*)out, b, s, q, h, d, l, p, shift, ntab, lv);
+  hipLaunchKernelGGL((deform_attn_gather_kernel<T, VEC, NC>), dim3((unsigned)blocks), dim3(kDeformThreads), lds,
+                     stream, (const T*)value, src, (T*)out, b, s, q, h, d, l, p, shift, ntab, lv);
   return hipGetLastError();
 }
 
-template <typename T, int VEC>
-static hipError_t pick_deform(const void* value, const void* loc, const void* attn, void* out, int b, int s, int q,
-                              int h, int d, int l, int p, const Levels& lv, hipStream_t stream) {
+template <typename T, int VEC, int NC>
+static hipError_t pick_deform(const void* value, PointSrc<T> src, void* out, int b, int s, int q, int h, int d, int l,
+                              int p, const Levels& lv, hipStream_t stream) {
   // byte offsets into value, plus a row, stay below the skip marker
   const long block_bytes = ((long)b * s * h * d + d) * (long)sizeof(T);
   if (d % VEC == 0 && block_bytes < (long)kDeformSkip)
-    return launch_gather<T, VEC>(value, loc, attn, out, b, s, q, h, d, l, p, lv, stream);
-  if (d % VEC == 0) return launch_deform<T, VEC>(value, loc, attn, out, b, s, q, h, d, l, p, lv, stream);
-  return launch_deform<T, 1>(value, loc, attn, out, b, s, q, h, d, l, p, lv, stream);
+    return launch_gather<T, VEC, NC>(value, src, out, b, s, q, h, d, l, p, lv, stream);
+  if (d % VEC == 0) return launch_deform<T, VEC, NC>(value, src, out, b, s, q, h, d, l, p, lv, stream);
+  return launch_deform<T, 1, NC>(value, src, out, b, s, q, h, d, l, p, lv, stream);
 }
 
-// Checked by the caller: 1 <= l <= 4, l * p <= 64, sum of level sizes == s, offsets fit in int32.
-hipError_t deform_attn(int dtype, const void* value, const void* loc, const void* attn, void* out, int b, int s,
-                       int q, int h, int d, int l, int p, const int* shapes, hipStream_t stream) {
+static Levels make_levels(int l, const int* shapes) {
   Levels lv{};
   int start = 0;
   for (int i = 0; i < l; ++i) {
@@ -273,9 +334,40 @@ hipError_t deform_attn(int dtype, const void* value, const void* loc, const void
     lv.start[i] = start;
     start += lv.h[i] * lv.w[i];
   }
-  if (dtype == kF32) return pick_deform<float, 4>(value, loc, attn, out, b, s, q, h, d, l, p, lv, stream);
-  if (dtype == kF16) return pick_deform<f16, 8>(value, loc, attn, out, b, s, q, h, d, l, p, lv, stream);
-  return pick_deform<bf16, 8>(value, loc, attn, out, b, s, q, h, d, l, p, lv, stream);
+  return lv;
+}
+
+template <typename T>
+static hipError_t pick_nc(const void* value, const void* a, const void* w, const void* refs, int nc, void* out, int b,
+                          int s, int q, int h, int d, int l, int p, const Levels& lv, hipStream_t stream) {
+  constexpr int VEC = 16 / sizeof(T);
+  const PointSrc<T> src{(const T*)a, (const T*)w, (const T*)refs, (float)(1.0 / (double)p)};
+  if (nc == 2) return pick_deform<T, VEC, 2>(value, src, out, b, s, q, h, d, l, p, lv, stream);
+  if (nc == 4) return pick_deform<T, VEC, 4>(value, src, out, b, s, q, h, d, l, p, lv, stream);
+  return pick_deform<T, VEC, 0>(value, src, out, b, s, q, h, d, l, p, lv, stream);
+}
+
+static hipError_t deform_dispatch(int dtype, const void* value, const void* a, const void* w, const void* refs, int nc,
+                                  void* out, int b, int s, int q, int h, int d, int l, int p, const int* shapes,
+                                  hipStream_t stream) {
+  const Levels lv = make_levels(l, shapes);
+  if (dtype == kF32) return pick_nc<float>(value, a, w, refs, nc, out, b, s, q, h, d, l, p, lv, stream);
+  if (dtype == kF16) return pick_nc<f16>(value, a, w, refs, nc, out, b, s, q, h, d, l, p, lv, stream);
+  return pick_nc<bf16>(value, a, w, refs, nc, out, b, s, q, h, d, l, p, lv, stream);
+}
+
+// Checked by the caller: 1 <= l <= 4, l * p <= 64, sum of level sizes == s, offsets fit in int32.
+hipError_t deform_attn(int dtype, const void* value, const void* loc, const void* attn, void* out, int b, int s,
+                       int q, int h, int d, int l, int p, const int* shapes, hipStream_t stream) {
+  return deform_dispatch(dtype, value, loc, attn, nullptr, 0, out, b, s, q, h, d, l, p, shapes, stream);
+}
+
+// Deform::forward between its projections: offsets, logits and reference points (ncoord 2 or 4) in
+// place of loc and attn. Same checks as deform_attn, plus ncoord in {2, 4}.
+hipError_t deform_core(int dtype, const void* value, const void* offsets, const void* logits, const void* refs,
+                       int ncoord, void* out, int b, int s, int q, int h, int d, int l, int p, const int* shapes,
+                       hipStream_t stream) {
+  return deform_dispatch(dtype, value, offsets, logits, refs, ncoord, out, b, s, q, h, d, l, p, shapes, stream);
 }
 
 }  // namespace samhip

@@ -17,6 +17,9 @@ hipError_t attn_relpos_f32(const void* q, const void* kt, const void* v, const v
                            int h, int w, float scale, hipStream_t stream);
 hipError_t deform_attn(int dtype, const void* value, const void* loc, const void* attn, void* out, int b, int s,
                        int q, int h, int d, int l, int p, const int* shapes, hipStream_t stream);
+hipError_t deform_core(int dtype, const void* value, const void* offsets, const void* logits, const void* refs,
+                       int ncoord, void* out, int b, int s, int q, int h, int d, int l, int p, const int* shapes,
+                       hipStream_t stream);
 hipError_t relpos_softmax(int dtype, const void* s, const void* q, const void* tab, void* out, long rows, int h, int w,
                           int hd, float scale, hipStream_t stream);
 hipError_t qkv_split(int dtype, const void* y, const void* bias, void* out, long tokens, int n, int nh, int hd,
@@ -96,9 +99,10 @@ int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void
   return check_launch(e, "attn-relpos");
 }
 
-int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, void* out, int dtype, int b, int s,
-                        int q, int h, int d, int l, int p, const int* shapes, void* stream) {
-  if (!value || !loc || !attn || !out || !shapes) return fail(SAM_HIP_EINVAL, "deform-attn: null pointer argument");
+namespace {
+// The argument checks shared by sam_hip_deform_attn and sam_hip_deform_core (pointers checked by the callers).
+int check_deform(const void* value, const void* out, int dtype, int b, int s, int q, int h, int d, int l, int p,
+                 const int* shapes) {
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (b <= 0 || s <= 0 || q <= 0 || h <= 0 || d <= 0 || l <= 0 || p <= 0)
     return fail(SAM_HIP_EINVAL, "deform-attn: sizes must be positive (b=%d s=%d q=%d h=%d d=%d l=%d p=%d)", b, s, q, h,
@@ -118,9 +122,30 @@ int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, vo
   // value rows are gathered and out rows stored in 16-byte vectors; loc and attn are read per element
   if (!aligned16(value) || !aligned16(out))
     return fail(SAM_HIP_EUNSUPPORTED, "deform-attn: value and out must be 16-byte aligned");
+  return SAM_HIP_OK;
+}
+}  // namespace
+
+int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, void* out, int dtype, int b, int s,
+                        int q, int h, int d, int l, int p, const int* shapes, void* stream) {
+  if (!value || !loc || !attn || !out || !shapes) return fail(SAM_HIP_EINVAL, "deform-attn: null pointer argument");
+  if (int rc = check_deform(value, out, dtype, b, s, q, h, d, l, p, shapes); rc != SAM_HIP_OK) return rc;
   hipError_t e = samhip::deform_attn(dtype, value, loc, attn, out, b, s, q, h, d, l, p, shapes,
                                      reinterpret_cast<hipStream_t>(stream));
   return check_launch(e, "deform-attn");
+}
+
+int sam_hip_deform_core(const void* value, const void* offsets, const void* logits, const void* refs, void* out,
+                        int dtype, int b, int s, int q, int h, int d, int l, int p, int ncoord, const int* shapes,
+                        void* stream) {
+  if (!value || !offsets || !logits || !refs || !out || !shapes)
+    return fail(SAM_HIP_EINVAL, "deform-core: null pointer argument");
+  if (ncoord != 2 && ncoord != 4)
+    return fail(SAM_HIP_EINVAL, "deform-core: reference points have 2 or 4 coordinates, got %d", ncoord);
+  if (int rc = check_deform(value, out, dtype, b, s, q, h, d, l, p, shapes); rc != SAM_HIP_OK) return rc;
+  hipError_t e = samhip::deform_core(dtype, value, offsets, logits, refs, ncoord, out, b, s, q, h, d, l, p, shapes,
+                                     reinterpret_cast<hipStream_t>(stream));
+  return check_launch(e, "deform-core");
 }
 
 int sam_hip_preprocess(const void* img, void* out, int dtype, int h, int w, int nh, int nw, int size,

@@ -8,6 +8,7 @@ Names, argument meaning and errors follow the reference:
     attention_relpos(q, kt, v, table, h, w, scale)       kernels.rs:899-906 (GPU: the fused kernel)
     qkv_split(y, bias, n, nh, hd)                        kernels.rs:872-894
     deform_attn(value, loc, attn, shapes)                kernels.rs:824-835
+    deform_core(value, offsets, logits, refs, shapes)    dino/mod.rs:166-179 (Deform::forward's core)
     flash_attn(q, k, v, scale=None)                      kernels.rs:910-915 / candle_flash_attn::flash_attn
     sdpa(q, k, v, mask=None)                             sam3/nn.rs:26-34
     rope(x, cos, sin)                                    sam3/video.rs:106-113
@@ -48,6 +49,8 @@ def load():
         L.sam_hip_attn_relpos.argtypes = [_vp] * 5 + [_i] * 5 + [_f, _vp]
         L.sam_hip_attn_relpos.restype = _i
         L.sam_hip_deform_attn.argtypes = [_vp] * 4 + [_i] * 8 + [ctypes.POINTER(ctypes.c_int), _vp]
+        L.sam_hip_deform_core.argtypes = [_vp] * 5 + [_i] * 9 + [ctypes.POINTER(ctypes.c_int), _vp]
+        L.sam_hip_deform_core.restype = _i
         L.sam_hip_bias_residual.argtypes = [_vp] * 4 + [_i, ctypes.c_long, _i, _vp]
         L.sam_hip_bias_residual.restype = _i
         L.sam_hip_bias_gelu.argtypes = [_vp] * 3 + [_i, ctypes.c_long, _i, _vp]
@@ -142,6 +145,32 @@ def deform_attn(value: torch.Tensor, loc: torch.Tensor, attn: torch.Tensor, shap
     out = torch.empty((b, q, h * d), dtype=value.dtype, device=value.device)
     _check(load().sam_hip_deform_attn(value.data_ptr(), loc.data_ptr(), attn.data_ptr(), out.data_ptr(), dt, b, s, q,
                                       h, d, l, p, flat, _stream()))
+    return out
+
+
+def deform_core(value: torch.Tensor, offsets: torch.Tensor, logits: torch.Tensor, refs: torch.Tensor,
+                shapes) -> torch.Tensor:
+    """Deform::forward between its projections (dino/mod.rs:166-179) in one kernel: logits
+    [B, Q, H, L, P] softmaxed over the L*P points, sampling locations from offsets [B, Q, H, L, P, 2]
+    and reference points refs [B, Q, L, 2] (encoder: ref + off / (W, H)) or [B, Q, L, 4] (decoder:
+    xy + off / P * wh * 0.5), then the bilinear gather of value [B, S, H, D] -> [B, Q, H*D]."""
+    value, offsets, logits, refs = (t.contiguous() for t in (value, offsets, logits, refs))
+    _contig(value, offsets, logits, refs)
+    dt = _dtype(value, offsets, logits, refs)
+    b, s, h, d = value.shape
+    if offsets.dim() != 6 or offsets.shape[0] != b or offsets.shape[2] != h or offsets.shape[5] != 2:
+        raise SamHipError(f"deform_core: offsets must be [B, Q, H, L, P, 2], got {tuple(offsets.shape)}")
+    q, l, p = offsets.shape[1], offsets.shape[3], offsets.shape[4]
+    if logits.shape != (b, q, h, l, p):
+        raise SamHipError(f"deform_core: logits must be {(b, q, h, l, p)}, got {tuple(logits.shape)}")
+    if refs.dim() != 4 or refs.shape[:3] != (b, q, l) or refs.shape[3] not in (2, 4):
+        raise SamHipError(f"deform_core: refs must be [B, Q, L, 2 or 4], got {tuple(refs.shape)}")
+    if len(shapes) != l:
+        raise SamHipError(f"deform_core: {len(shapes)} level shapes for {l} levels")
+    flat = (ctypes.c_int * (2 * l))(*[int(x) for hw in shapes for x in hw])
+    out = torch.empty((b, q, h * d), dtype=value.dtype, device=value.device)
+    _check(load().sam_hip_deform_core(value.data_ptr(), offsets.data_ptr(), logits.data_ptr(), refs.data_ptr(),
+                                      out.data_ptr(), dt, b, s, q, h, d, l, p, refs.shape[3], flat, _stream()))
     return out
 
 

@@ -10,6 +10,9 @@ oracle's restatement of the reference:
   formulation so the two can be compared exactly;
 * deformable attention is the scalar ``grid_sample(align_corners=False, padding_mode="zeros")`` loop of
   the reference's own test (tests/dino.rs:9-40) and, separately, torch's ``grid_sample``;
+* the deformable-attention module's sampling locations and weights (Deform::forward) follow the
+  Deformable-DETR formulation with torch broadcasting (offset normaliser stacked as (W, H), box refs as
+  ``xy + off / P * wh * 0.5``), in float64;
 * attention without bias uses torch's ``scaled_dot_product_attention`` in float64;
 * RoPE uses the complex-number (polar) formulation of 2-D axial rotary embeddings.
 """
@@ -136,6 +139,26 @@ def deform_grid_sample64(value, loc, attn, shapes) -> np.ndarray:
     a = attn.transpose(1, 2).reshape(b * h, 1, q, l * p)
     out = (torch.stack(samples, dim=-2).flatten(-2) * a).sum(-1).view(b, h * d, q)
     return out.transpose(1, 2).contiguous().numpy()
+
+
+def deform_prep64(off, logits, refs, shapes):
+    """Sampling locations and attention weights of a multi-scale deformable attention module, float64:
+    weights = softmax over the L*P points; 2-coordinate refs: ref + off / (W_l, H_l); 4-coordinate
+    (box) refs: xy + off / P * wh * 0.5. off [B,Q,H,L,P,2], logits [B,Q,H,L,P], refs [B,Q,L,2|4]."""
+    import torch
+
+    off = torch.as_tensor(np.asarray(off, np.float64))
+    logits = torch.as_tensor(np.asarray(logits, np.float64))
+    refs = torch.as_tensor(np.asarray(refs, np.float64))
+    b, q, h, l, p, _ = off.shape
+    attn = torch.softmax(logits.reshape(b, q, h, l * p), -1).reshape(b, q, h, l, p)
+    shp = torch.as_tensor(np.asarray(shapes, np.float64))  # (H_l, W_l)
+    if refs.shape[-1] == 2:
+        norm = torch.stack([shp[:, 1], shp[:, 0]], -1)  # (W_l, H_l)
+        loc = refs[:, :, None, :, None, :] + off / norm[None, None, None, :, None, :]
+    else:
+        loc = refs[:, :, None, :, None, :2] + off / p * refs[:, :, None, :, None, 2:] * 0.5
+    return loc.numpy(), attn.numpy()
 
 
 def sdpa64(q, k, v, scale: float | None = None) -> np.ndarray:

@@ -184,6 +184,79 @@ def test_deform_matches_scalar_spec_and_grid_sample(oracle_lib, shapes, b, q, h,
     assert np.abs(got - naive).max() < 1e-5
 
 
+def _prep_inputs(shapes, b, q, h, p, nc, seed):
+    r = _rng(seed)
+    l = len(shapes)
+    off = (2.0 * r.standard_normal((b, q, h, l, p, 2))).astype(np.float32)  # ~N(0,2) pixels
+    logits = r.standard_normal((b, q, h, l, p)).astype(np.float32)
+    if nc == 2:
+        refs = r.uniform(0, 1, (b, q, l, 2)).astype(np.float32)
+    else:
+        refs = np.concatenate([r.uniform(0.1, 0.9, (b, q, l, 2)), r.uniform(0.05, 0.5, (b, q, l, 2))], -1)
+        refs = refs.astype(np.float32)
+    return off, logits, refs
+
+
+# Non-square levels (a swapped (W, H) normaliser would show), the DINO point count and an odd one.
+PREP_CASES = [([(7, 9), (4, 5), (2, 3)], 1, 13, 4, 3), ([(9, 12), (5, 6), (3, 3), (2, 2)], 1, 37, 8, 4),
+              ([(5, 4), (3, 2)], 2, 6, 2, 2)]
+
+
+@pytest.mark.parametrize("nc", [2, 4])
+@pytest.mark.parametrize("shapes,b,q,h,p", PREP_CASES)
+def test_deform_prep_matches_float64_module(oracle_lib, shapes, b, q, h, p, nc):
+    """dino/mod.rs:166-178 against the Deformable-DETR formulation in float64, then the whole core
+    (prep + gather) against torch's grid_sample."""
+    off, logits, refs = _prep_inputs(shapes, b, q, h, p, nc, 40 + q + nc)
+    loc, attn = oracle_lib.deform_prep(off, logits, refs, shapes)
+    loc64, attn64 = refimpl.deform_prep64(off, logits, refs, shapes)
+    assert np.abs(loc - loc64).max() < 2e-6
+    assert np.abs(attn - attn64).max() < 1e-6
+    np.testing.assert_allclose(attn.sum(-1).sum(-1), 1.0, atol=2e-6)
+    value = _rng(7).standard_normal((b, sum(hh * ww for hh, ww in shapes), h, 8)).astype(np.float32)
+    got = oracle_lib.deform_forward_core(value, off, logits, refs, shapes)
+    want = refimpl.deform_grid_sample64(value, loc64, attn64, shapes)
+    assert np.abs(got - want).max() < 2e-5
+
+
+def test_deform_prep_closed_forms(oracle_lib):
+    """Zero offsets sample at the reference point; an offset of one level size moves the encoder form
+    by exactly 1; an offset of 2P moves the decoder form by exactly the box size; equal logits give
+    equal weights 1 / (L*P)."""
+    shapes = [(6, 10), (3, 5)]
+    b, q, h, p = 1, 5, 2, 4
+    l = len(shapes)
+    off, logits, refs2 = _prep_inputs(shapes, b, q, h, p, 2, 3)
+    _, _, refs4 = _prep_inputs(shapes, b, q, h, p, 4, 4)
+    zero = np.zeros_like(off)
+    loc, attn = oracle_lib.deform_prep(zero, np.zeros_like(logits), refs2, shapes)
+    assert np.array_equal(loc, np.broadcast_to(refs2[:, :, None, :, None, :], loc.shape))
+    assert np.array_equal(attn, np.full_like(attn, np.float32(1.0 / (l * p))))
+    loc, _ = oracle_lib.deform_prep(zero, logits, refs4, shapes)
+    assert np.array_equal(loc, np.broadcast_to(refs4[:, :, None, :, None, :2], loc.shape))
+    one = np.empty_like(off)
+    for li, (hh, ww) in enumerate(shapes):
+        one[:, :, :, li, :, 0] = ww
+        one[:, :, :, li, :, 1] = hh
+    loc, _ = oracle_lib.deform_prep(one, logits, refs2, shapes)
+    assert np.array_equal(loc, np.broadcast_to(refs2[:, :, None, :, None, :] + np.float32(1), loc.shape))
+    loc, _ = oracle_lib.deform_prep(np.full_like(off, 2.0 * p), logits, refs4, shapes)
+    xy, wh = refs4[:, :, None, :, None, :2], refs4[:, :, None, :, None, 2:]
+    assert np.array_equal(loc, np.broadcast_to(xy + wh, loc.shape))
+
+
+def test_deform_prep_rejects_a_swapped_normaliser(oracle_lib):
+    """A planted mistake, (H, W) in place of (W, H), is caught by the float64 module on non-square
+    levels."""
+    shapes = [(7, 9), (4, 5)]
+    off, logits, refs = _prep_inputs(shapes, 1, 9, 2, 4, 2, 5)
+    loc, _ = oracle_lib.deform_prep(off, logits, refs, shapes)
+    swapped, _ = oracle_lib.deform_prep(off, logits, refs, [(w, h) for h, w in shapes])
+    loc64, _ = refimpl.deform_prep64(off, logits, refs, shapes)
+    assert np.abs(loc - loc64).max() < 2e-6
+    assert np.abs(swapped[..., 0] - loc64[..., 0]).max() > 1e-3
+
+
 def test_deform_pixel_centres_are_a_pure_gather(oracle_lib):
     shapes = [(6, 8), (3, 4)]
     b, q, h, d, p = 1, 5, 2, 4, 2
