@@ -234,6 +234,52 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
 
+        # the same layer through Deform::forward's fused core: offsets, logits and reference points in
+        # place of loc and attn (softmax and sampling locations formed in the kernel)
+        refs = (ref.view(1, q, 1, 2).expand(1, q, ll, 2) if name == "encoder" else
+                torch.cat([ref.view(1, q, 1, 2), 0.05 + 0.5 * torch.rand(1, q, 1, 2, device=dev, generator=g)],
+                          -1).expand(1, q, ll, 4)).contiguous()
+        logits = torch.randn(1, q, hh, ll, pp, device=dev, generator=g)
+
+        def run_core():
+            check(lib, lib.sam_hip_deform_core(value.data_ptr(), off.data_ptr(), logits.data_ptr(), refs.data_ptr(),
+                                               out.data_ptr(), 0, 1, s, q, hh, dd, ll, pp, refs.shape[3], flat, sp))
+
+        ms = timer.avg_ms(run_core, 50)
+        nbytes = 4.0 * (s * hh * dd + 3 * q * hh * ll * pp + q * ll * refs.shape[3] + q * hh * dd)
+        res[f"dino_deform_core_{name}_f32"] = {
+            "workload": f"Grounding DINO-tiny Deform::forward core (logit softmax + {refs.shape[3]}-coordinate "
+                        f"sampling locations + gather), {q} queries over {s} values, 8 heads x 32, 4 levels x 4 points",
+            "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+
+    # relpos_softmax (the reference's GPU step between its two bmm calls) over materialised f16 scores:
+    # a ViT-H global layer (16 heads x 4096 rows of 4096) and a windowed layer (400 units x 196 rows of
+    # 196). Compulsory bytes: the scores read once and the probabilities written once (q and the table
+    # add under 1%).
+    for name, (bh, side) in (("global", (16, 64)), ("window", (400, 14))):
+        n = side * side
+        sc = torch.randn(bh, n, n, device=dev, generator=g).half()
+        qq = torch.randn(bh, n, HD, device=dev, generator=g).half()
+        tb = (0.02 * torch.randn(4 * side - 2, HD, device=dev, generator=g)).half()
+        pr = torch.empty_like(sc)
+
+        def run():
+            check(lib, lib.sam_hip_relpos_softmax(sc.data_ptr(), qq.data_ptr(), tb.data_ptr(), pr.data_ptr(), 1,
+                                                  bh * n, side, side, HD, HD ** -0.5, sp))
+
+        ms = timer.avg_ms(run, 20)
+        nbytes = 2.0 * bh * n * n * 2 + bh * n * HD * 2
+        res[f"vit_h_relpos_softmax_{name}_f16"] = {
+            "workload": f"SAM ViT-H relpos_softmax over materialised scores, {bh} x {n} rows of {n}, hd {HD}, f16",
+            "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        del sc, pr
+
     # SAM image preprocessing (image_proc::prepare): a u8 RGB image resized so its longest side is 1024,
     # normalised and zero padded into [1, 3, 1024, 1024], for a 1920x1080 frame and a 4000x3000 photo.
     for name, (ih, iw) in (("1080p", (1080, 1920)), ("12mp", (3000, 4000))):

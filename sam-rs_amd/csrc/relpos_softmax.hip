@@ -1,154 +1,463 @@
 // Softmax over materialised scores with the decomposed relative-position bias, for gfx950:
 //
-//   out[bh, r, k] = softmax_k( scale * s[bh, r, k] + q[bh, r] . Th[i - kh + H-1] + q[bh, r] . Tw[j - kw + W-1] )
+//   out[r, k] = softmax_k( scale * s[r, k] + q[r] . Th[i - kh + H-1] + q[r] . Tw[j - kw + W-1] )
 //
-// with r = i*W + j, k = kh*W + kw. This is the reference's relpos_softmax (kernels.rs:12-43, GPU kernel
-// sam.cu:44-96, CPU twin kernels.rs:62-105), kept for callers that already hold the score matrix; the
-// fused attention (attn_relpos.hip) never materialises it.
+// for score rows r (i = (r mod N) / W, j = r mod W, N = H*W) and keys k = kh*W + kw. This is the
+// contract of the reference's relpos_softmax (kernels.rs:12-43; its CPU twin kernels.rs:62-105), for
+// callers that already hold the score matrix; the fused attention never materialises it.
 //
-// One workgroup of 256 threads per score row (as the reference), the row held in registers (ITEMS
-// values per thread, N <= 256 * ITEMS). The H + W bias dot products are spread over the threads
-// (one each), with q staged in LDS; max and sum are reduced across each wave with DPP row shifts and
-// permlane32_swap, then across the 4 waves through LDS. The row is read and written once: the kernel
-// is bound by HBM (2 * N elements per row).
+// The work is streaming: each row is read once and written once (2 * N elements), so the kernel is
+// built around HBM traffic rather than arithmetic.
+//   * A wave owns 32 consecutive rows. Their bias dot products are one small GEMM, G = Table . Q^T
+//     (all (2H-1) + (2W-1) table rows against the 32 q rows), on the MFMA (32x32x16 f16/bf16,
+//     32x32x2 f32), one 32-row block of the table at a time. Each lane then holds one q row's
+//     products with 16 table rows and scatters those that fall on the row's diagonal band into a
+//     wave-private LDS array, bias[row][kw] (Rw) and bias[row][W + kh] (Rh). q rows are indexed by the
+//     global row r, so a wave's rows may straddle windows or heads.
+//   * Rows then stream through registers as 16-byte (or, when a row is not a multiple of 16 bytes,
+//     8-byte) vectors: a lane owns vectors lane, lane + 64, ...; a vector's (kh, kw) is fixed per lane
+//     for all rows. Max and sum are reduced over the wave on the VALU (DPP row rotations, then
+//     v_permlane16_swap and v_permlane32_swap); no LDS reductions and no workgroup barriers.
+//   * Several rows are in flight per wave: rows are loaded in groups of up to 8 vectors per lane, two
+//     groups ahead of the one being computed (a ring of three register buffers).
+//   * Rows that are not a multiple of 8 bytes, or that would need more than 16 vectors per lane, take a
+//     two-pass loop (online max and sum, then the outputs) over scalars.
+// Arithmetic: the logit is (s * scale + Rh) + Rw with separate f32 roundings, as the reference's CPU
+// path computes it; exp(x - max) as exp2((x - max) * log2 e); P = e * (1 / sum).
 #include "common.hpp"
+
+#pragma clang diagnostic ignored "-Wunused-parameter"
 
 namespace samhip {
 
-constexpr int kSmThreads = 256;
+namespace rsm {
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWaves = 4;   // waves per workgroup (independent)
+constexpr int kRows = 32;   // rows per wave
+}  // namespace rsm
 
-__device__ __forceinline__ float wave_max(float v) {
-  // within rows of 16 lanes, then across the 4 rows of a wave
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return max_with_partner32(v);
+// Wave64 reductions on the VALU, with no LDS round trip: DPP row rotations by 1, 2, 4 and 8 reduce each
+// row of 16 lanes (every lane ends with its row's result), then v_permlane16_swap and
+// v_permlane32_swap combine the rows.
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 | N, 0xf, 0xf, false));
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
-  v += __shfl_xor(v, 16, 64);
-  return sum_with_partner32(v);
+__device__ __forceinline__ float partner16(float v, bool take_max) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return take_max ? fmaxf(a, b) : a + b;
+}
+__device__ __forceinline__ float wave_max64(float v) {
+  v = fmaxf(v, row_ror<1>(v));
+  v = fmaxf(v, row_ror<2>(v));
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<8>(v));
+  return max_with_partner32(partner16(v, true));
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+  v += row_ror<1>(v);
+  v += row_ror<2>(v);
+  v += row_ror<4>(v);
+  v += row_ror<8>(v);
+  return sum_with_partner32(partner16(v, false));
 }
 
-template <typename T, int ITEMS, bool VEC8>
-__global__ __launch_bounds__(kSmThreads) void relpos_softmax_kernel(const T* __restrict__ s, const T* __restrict__ q,
-                                                                   const T* __restrict__ tab, T* __restrict__ out,
-                                                                   int H, int W, int HD, float scale) {
-  __shared__ float qs[256];  // hd <= 256
-  __shared__ float rh[128], rw[128];
-  __shared__ float red[2][4];
-  const int N = H * W;
-  const long row = blockIdx.x;
-  const int rem = (int)(row % N), i = rem / W, j = rem % W;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int c = tid; c < HD; c += kSmThreads) qs[c] = to_f32(q[row * HD + c]);
-  __syncthreads();
-  if (tid < H + W) {
-    const bool is_h = tid < H;
-    const int kk = is_h ? tid : tid - H;
-    const T* tr = tab + (is_h ? (long)(i - kk + H - 1) : (long)(2 * H - 1) + (j - kk + W - 1)) * HD;
-    float a = 0.f;
-    for (int c = 0; c < HD; ++c) a += qs[c] * to_f32(tr[c]);
-    (is_h ? rh : rw)[kk] = a;
+// 8 consecutive elements of a row of `ld` elements (zero past `len`), as an MFMA operand.
+template <typename T>
+__device__ __forceinline__ typename Vec<T>::x8 load8(const T* row, int k, int len, bool vec) {
+  typedef typename Vec<T>::x8 X8;
+  if (vec && k + 8 <= len) return *reinterpret_cast<const X8*>(row + k);
+  X8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = k + e < len ? row[k + e] : (T)0.f;
+  return r;
+}
+
+// The wave's bias rows: bias[row][0 .. W) = Rw, bias[row][W .. W+H) = Rh, row pitch bst floats (a
+// multiple of 4, so a row's Rw run can be read as 16-byte vectors). Lane l holds, per 32-row block tb of
+// the table, G[tb + m][row n] for m = 8 (e/4) + 4 (l/32) + e%4 (n = l % 32), the products of the wave's
+// q row n with table rows tb .. tb+31, and scatters those on the row's diagonal band.
+__device__ __forceinline__ void scatter_band(const f32x16& g, float* brow, int tb, int hh, int i, int j, int H,
+                                             int W) {
+  const int th = 2 * H - 1, trows = th + 2 * W - 1;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int tr = tb + 8 * (e >> 2) + 4 * hh + (e & 3);
+    if (tr < th) {
+      const int kh = i + H - 1 - tr;
+      if (kh >= 0 && kh < H) brow[W + kh] = g[e];
+    } else if (tr < trows) {
+      const int kw = j + W - 1 - (tr - th);
+      if (kw >= 0 && kw < W) brow[kw] = g[e];
+    }
   }
-  __syncthreads();
+}
 
-  // element k of this thread's t-th chunk: k = (t * 256 + tid) * CH + e, CH = 8 (vector) or 1
-  constexpr int CH = VEC8 ? 8 : 1;
-  constexpr int NCH = ITEMS / CH;
-  const T* sr = s + row * N;
-  float x[ITEMS];
-  float m = -INFINITY;
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Head dims up to 128 and a multiple of 8 (SAM's 64 and 80): the q fragments are loaded once, and
+// every operand load of a table block is issued before its MFMAs, so the prologue waits on memory
+// about once per block instead of once per k-step. Rows past the table read its last row (not
+// scattered).
+template <typename T>
+__device__ __forceinline__ void build_bias_short(const T* qrow, const T* tab, float* brow, int i, int j, int H, int W,
+                                                 int HD) {
+  const int lane = threadIdx.x & 63, n = lane & 31, hh = lane >> 5;
+  const int trows = 2 * H - 1 + 2 * W - 1;
+  if constexpr (__is_same(T, float)) {
+    // 32x32x2 f32: MFMA step t pairs dim t (lanes 0-31) with dim HD/2 + t (lanes 32-63) of the q row
+    // (B) and of the table row (A); HD/2 is a multiple of 4, so each half moves as 16-byte vectors
+    const int half = HD / 2, base = hh * half;
+    float qv[64];
 #pragma unroll
-  for (int t = 0; t < NCH; ++t) {
-    const int k0 = (t * kSmThreads + tid) * CH;
-    if (VEC8) {
-      typename Vec<T>::x8 v8 = {};
-      if (k0 < N) v8 = *reinterpret_cast<const typename Vec<T>::x8*>(sr + k0);
+    for (int c = 0; c < 64; c += 4) {
+      const f32x4 v = c < half ? *reinterpret_cast<const f32x4*>(qrow + base + c) : f32x4{};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int k = k0 + e;
-        float val = -INFINITY;
-        if (k < N) {
-          const int kh = k / W, kw = k - kh * W;
-          val = to_f32(v8[e]) * scale + rh[kh] + rw[kw];
-        }
-        x[t * 8 + e] = val;
-        m = fmaxf(m, val);
+      for (int u = 0; u < 4; ++u) qv[c + u] = v[u];
+    }
+    for (int tb = 0; tb < trows; tb += 32) {
+      const float* trow = tab + (long)min(tb + n, trows - 1) * HD;
+      float tv[64];
+#pragma unroll
+      for (int c = 0; c < 64; c += 4) {
+        const f32x4 v = c < half ? *reinterpret_cast<const f32x4*>(trow + base + c) : f32x4{};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) tv[c + u] = v[u];
+      }
+      f32x16 g = f32x16{};
+#pragma unroll
+      for (int t = 0; t < 64; ++t)
+        if (t < half) g = __builtin_amdgcn_mfma_f32_32x32x2f32(tv[t], qv[t], g, 0, 0, 0);
+      scatter_band(g, brow, tb, hh, i, j, H, W);
+    }
+  } else {
+    typedef typename Vec<T>::x8 X8;
+    const int ks = (HD + 15) / 16;  // k-steps; at HD % 16 == 8 the last one's upper half is zero
+    X8 qf[8], a[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int k = 16 * s + 8 * hh;
+      qf[s] = k < HD ? *reinterpret_cast<const X8*>(qrow + k) : X8{};
+    }
+    for (int tb = 0; tb < trows; tb += 32) {
+      const T* trow = tab + (long)min(tb + n, trows - 1) * HD;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int k = 16 * s + 8 * hh;
+        a[s] = k < HD ? *reinterpret_cast<const X8*>(trow + k) : X8{};
+      }
+      f32x16 g = f32x16{};
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        if (s < ks) g = mma32(a[s], qf[s], g);
+      scatter_band(g, brow, tb, hh, i, j, H, W);
+    }
+  }
+}
+
+// Any head dim (up to 256): one k-step at a time.
+template <typename T>
+__device__ __forceinline__ void build_bias_long(const T* qrow, const T* tab, float* brow, int i, int j, int H, int W,
+                                                int HD) {
+  const int lane = threadIdx.x & 63, n = lane & 31, hh = lane >> 5;
+  const int trows = 2 * H - 1 + 2 * W - 1;
+  for (int tb = 0; tb < trows; tb += 32) {
+    const T* trow = tab + (long)min(tb + n, trows - 1) * HD;
+    f32x16 g = f32x16{};
+    if constexpr (__is_same(T, float)) {
+      for (int k0 = 0; k0 < HD; k0 += 2) {
+        const int k = k0 + hh;
+        g = __builtin_amdgcn_mfma_f32_32x32x2f32(k < HD ? trow[k] : 0.f, k < HD ? qrow[k] : 0.f, g, 0, 0, 0);
       }
     } else {
-      float val = -INFINITY;
-      if (k0 < N) {
-        const int kh = k0 / W, kw = k0 - kh * W;
-        val = to_f32(sr[k0]) * scale + rh[kh] + rw[kw];
+      for (int k0 = 0; k0 < HD; k0 += 16) {
+        const int k = k0 + 8 * hh;
+        g = mma32(load8(trow, k, HD, HD % 8 == 0), load8(qrow, k, HD, HD % 8 == 0), g);
       }
-      x[t] = val;
-      m = fmaxf(m, val);
     }
+    scatter_band(g, brow, tb, hh, i, j, H, W);
   }
-  m = wave_max(m);
-  if (lane == 0) red[0][wave] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-  float sum = 0.f;
-#pragma unroll
-  for (int t = 0; t < ITEMS; ++t) {
-    const float e = __expf(x[t] - m);
-    x[t] = e;
-    sum += e;
-  }
-  sum = wave_sum(sum);
-  if (lane == 0) red[1][wave] = sum;
-  __syncthreads();
-  const float inv = 1.f / (red[1][0] + red[1][1] + red[1][2] + red[1][3]);
-  T* orow = out + row * N;
-#pragma unroll
-  for (int t = 0; t < NCH; ++t) {
-    const int k0 = (t * kSmThreads + tid) * CH;
-    if (VEC8) {
-      if (k0 < N) {
-        typename Vec<T>::x8 v8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v8[e] = from_f32<T>(x[t * 8 + e] * inv);
-        *reinterpret_cast<typename Vec<T>::x8*>(orow + k0) = v8;
-      }
-    } else if (k0 < N) {
-      orow[k0] = from_f32<T>(x[t] * inv);
-    }
-  }
-}
-
-template <typename T, int ITEMS>
-static hipError_t launch_sm(const void* s, const void* q, const void* tab, void* out, long rows, int h, int w, int hd,
-                            float scale, hipStream_t stream) {
-  const int n = h * w;
-  if (n % 8 == 0 && ITEMS >= 8)
-    hipLaunchKernelGGL((relpos_softmax_kernel<T, ITEMS, true>), dim3((unsigned)rows), dim3(kSmThreads), 0, stream,
-                       (const T*)s, (const T*)q, (const T*)tab, (T*)out, h, w, hd, scale);
-  else
-    hipLaunchKernelGGL((relpos_softmax_kernel<T, ITEMS, false>), dim3((unsigned)rows), dim3(kSmThreads), 0, stream,
-                       (const T*)s, (const T*)q, (const T*)tab, (T*)out, h, w, hd, scale);
-  return hipGetLastError();
 }
 
 template <typename T>
-static hipError_t pick_items(const void* s, const void* q, const void* tab, void* out, long rows, int h, int w, int hd,
-                             float scale, hipStream_t stream) {
-  const int n = h * w;
-  // the vector path needs ITEMS a multiple of 8; the scalar path takes any ITEMS
-  if (n <= 256) return launch_sm<T, 1>(s, q, tab, out, rows, h, w, hd, scale, stream);
-  if (n <= 2048) return launch_sm<T, 8>(s, q, tab, out, rows, h, w, hd, scale, stream);
-  if (n <= 4096) return launch_sm<T, 16>(s, q, tab, out, rows, h, w, hd, scale, stream);
-  return launch_sm<T, 32>(s, q, tab, out, rows, h, w, hd, scale, stream);
+__device__ __forceinline__ void build_bias(const T* q, const T* tab, float* bias, long r0, long rows, int H, int W,
+                                           int HD, int bst) {
+  const int lane = threadIdx.x & 63, n = lane & 31;
+  const int N = H * W;
+  const long rq = min(r0 + n, rows - 1);
+  const int rem = (int)(rq % N);
+  const int i = rem / W, j = rem - (rem / W) * W;
+  const T* qrow = q + rq * HD;
+  float* brow = bias + n * bst;
+  if (HD <= 128 && HD % 8 == 0)
+    build_bias_short(qrow, tab, brow, i, j, H, W, HD);
+  else
+    build_bias_long(qrow, tab, brow, i, j, H, W, HD);
+  wave_sync();
 }
 
-// Checked by the caller: n = h*w <= 8192, h, w <= 128, hd <= 256.
+template <typename T, int VB> struct Raw;  // VB bytes of a row as loaded
+template <typename T> struct Raw<T, 16> { typedef u32x4 type; };
+template <typename T> struct Raw<T, 8> { typedef u32x2 type; };
+
+template <typename T, int VB>
+__device__ __forceinline__ float raw_elem(const typename Raw<T, VB>::type& v, int e) {
+  typedef T TV __attribute__((ext_vector_type(VB / sizeof(T))));
+  return to_f32(__builtin_bit_cast(TV, v)[e]);
+}
+
+// Vectorised rows: VB-byte vectors of VE = VB / sizeof(T) elements, ITEMS vectors per lane and row.
+// AW: W is a multiple of VE, so every vector lies in one grid row (one Rh value, VE consecutive Rw).
+template <typename T, int VB, int ITEMS, bool AW>
+__global__ __launch_bounds__(rsm::kWaves * 64) void relpos_softmax_vec_kernel(const T* __restrict__ s,
+                                                                             const T* __restrict__ q,
+                                                                             const T* __restrict__ tab,
+                                                                             T* __restrict__ out, long rows, int H,
+                                                                             int W, int HD, float scale, int bst) {
+#pragma clang fp contract(off)
+  using namespace rsm;
+  typedef typename Raw<T, VB>::type RV;
+  constexpr int VE = VB / (int)sizeof(T);
+  constexpr int G = ITEMS >= 8 ? 1 : 8 / ITEMS;  // rows per load group
+  static_assert(!AW || VE % 4 == 0, "vector Rw reads cover whole 16-byte runs");
+  extern __shared__ float bias_lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long r0 = ((long)blockIdx.x * kWaves + wave) * kRows;
+  if (r0 >= rows) return;  // the waves of a workgroup share nothing
+  float* bias = bias_lds + wave * kRows * bst;
+  const int N = H * W, nvec = N / VE;
+  const int nrows = (int)min((long)kRows, rows - r0);
+  // (kh << 16 | kw) of the first element of each of this lane's vectors: the same for every row
+  int khw[ITEMS];
+#pragma unroll
+  for (int t = 0; t < ITEMS; ++t) {
+    const int k = (lane + 64 * t) * VE;
+    const int kh = k / W;
+    khw[t] = (kh << 16) | (k - kh * W);
+  }
+  auto load_group = [&](int g0, RV (&buf)[G][ITEMS]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int rl = g0 + g;
+      const T* srow = s + (r0 + (rl < nrows ? rl : 0)) * (long)N;
+#pragma unroll
+      for (int t = 0; t < ITEMS; ++t) {
+        const int v = lane + 64 * t;
+        buf[g][t] = v < nvec ? *reinterpret_cast<const RV*>(srow + v * VE) : RV{};
+      }
+    }
+  };
+  // logits of row g0 + g into x (padding lanes -inf); returns this lane's max
+  auto logits = [&](int rl, const RV (&raw)[ITEMS], float (&x)[ITEMS][VE]) {
+    const float* brow = bias + min(rl, nrows - 1) * bst;
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < ITEMS; ++t) {
+      const bool ok = lane + 64 * t < nvec;
+      int kh = khw[t] >> 16, kw = khw[t] & 0xffff;
+      if constexpr (AW) {
+        const float rh = brow[W + kh];
+        float rw[VE];
+#pragma unroll
+        for (int e4 = 0; e4 < VE; e4 += 4) {
+          const f32x4 r4 = *reinterpret_cast<const f32x4*>(brow + kw + e4);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) rw[e4 + u] = r4[u];
+        }
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+          const float v = (raw_elem<T, VB>(raw[t], e) * scale + rh) + rw[e];
+          x[t][e] = ok ? v : -INFINITY;
+          m = fmaxf(m, x[t][e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+          const float v = (raw_elem<T, VB>(raw[t], e) * scale + brow[W + kh]) + brow[kw];
+          x[t][e] = ok ? v : -INFINITY;
+          m = fmaxf(m, x[t][e]);
+          if (++kw == W) {
+            kw = 0;
+            ++kh;
+          }
+        }
+      }
+    }
+    return m;
+  };
+  // the reductions, exponentials and stores of a whole group: each step runs for all of the group's
+  // rows before the next, so the rows' cross-lane exchanges overlap (one basic block, no early exits)
+  auto finish = [&](int g0, float (&x)[G][ITEMS][VE], float (&m)[G]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) m[g] = wave_max64(m[g]);
+    float sum[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      sum[g] = 0.f;
+#pragma unroll
+      for (int t = 0; t < ITEMS; ++t)
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+          x[g][t][e] = exp2_fast((x[g][t][e] - m[g]) * kLog2e);
+          sum[g] += x[g][t][e];
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) sum[g] = 1.f / wave_sum64(sum[g]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      T* orow = out + (r0 + min(g0 + g, nrows - 1)) * (long)N;
+#pragma unroll
+      for (int t = 0; t < ITEMS; ++t) {
+        const int v = lane + 64 * t;
+        if (v < nvec && g0 + g < nrows) {
+          typedef T TV __attribute__((ext_vector_type(VE)));
+          TV o;
+#pragma unroll
+          for (int e = 0; e < VE; ++e) o[e] = from_f32<T>(x[g][t][e] * sum[g]);
+          *reinterpret_cast<TV*>(orow + v * VE) = o;
+        }
+      }
+    }
+  };
+  // A ring of three load buffers: two groups are in flight while a third is computed. A group's buffer
+  // is refilled (with the group three ahead) as soon as its logits are formed, so the loads land while
+  // this group's reductions, exponentials and stores run and while the next group is computed. The
+  // first two groups' loads go out before the bias prologue.
+  RV b0[G][ITEMS], b1[G][ITEMS], b2[G][ITEMS];
+  load_group(0, b0);
+  if (G < nrows) load_group(G, b1);
+  build_bias(q, tab, bias, r0, rows, H, W, HD, bst);
+  auto step = [&](int g0, RV (&cur)[G][ITEMS], RV (&spare)[G][ITEMS]) {
+    if (g0 >= nrows) return;
+    float x[G][ITEMS][VE], m[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) m[g] = logits(g0 + g, cur[g], x[g]);
+    if (g0 + 2 * G < nrows) load_group(g0 + 2 * G, spare);
+    finish(g0, x, m);
+  };
+  for (int g0 = 0; g0 < nrows; g0 += 3 * G) {
+    step(g0, b0, b2);
+    step(g0 + G, b1, b0);
+    step(g0 + 2 * G, b2, b1);
+  }
+}
+
+// Any row length: an online (max, sum) pass over the row, then a pass that writes the outputs.
+template <typename T>
+__global__ __launch_bounds__(rsm::kWaves * 64) void relpos_softmax_scalar_kernel(const T* __restrict__ s,
+                                                                                const T* __restrict__ q,
+                                                                                const T* __restrict__ tab,
+                                                                                T* __restrict__ out, long rows,
+                                                                                int H, int W, int HD, float scale,
+                                                                                int bst) {
+#pragma clang fp contract(off)
+  using namespace rsm;
+  extern __shared__ float bias_lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long r0 = ((long)blockIdx.x * kWaves + wave) * kRows;
+  if (r0 >= rows) return;
+  float* bias = bias_lds + wave * kRows * bst;
+  build_bias(q, tab, bias, r0, rows, H, W, HD, bst);
+  const int N = H * W;
+  const int nrows = (int)min((long)kRows, rows - r0);
+  for (int rl = 0; rl < nrows; ++rl) {
+    const T* srow = s + (r0 + rl) * (long)N;
+    const float* brow = bias + rl * bst;
+    float m = -INFINITY, sum = 0.f;
+    for (int k = lane; k < N; k += 64) {
+      const int kh = k / W, kw = k - kh * W;
+      const float x = (to_f32(srow[k]) * scale + brow[W + kh]) + brow[kw];
+      if (x > m) {
+        sum = sum * exp2_fast((m - x) * kLog2e) + 1.f;
+        m = x;
+      } else {
+        sum += exp2_fast((x - m) * kLog2e);
+      }
+    }
+    const float mw = wave_max64(m);
+    sum = m == -INFINITY ? 0.f : sum * exp2_fast((m - mw) * kLog2e);
+    const float inv = 1.f / wave_sum64(sum);
+    T* orow = out + (r0 + rl) * (long)N;
+    for (int k = lane; k < N; k += 64) {
+      const int kh = k / W, kw = k - kh * W;
+      const float x = (to_f32(srow[k]) * scale + brow[W + kh]) + brow[kw];
+      orow[k] = from_f32<T>(exp2_fast((x - mw) * kLog2e) * inv);
+    }
+  }
+}
+
+template <typename T, int VB, int ITEMS, bool AW>
+static hipError_t launch_vec(const void* s, const void* q, const void* tab, void* out, long rows, int h, int w, int hd,
+                             float scale, unsigned blocks, size_t lds, int bst, hipStream_t stream) {
+  auto kern = relpos_softmax_vec_kernel<T, VB, ITEMS, AW>;
+  static std::atomic<unsigned long long> done{0};
+  if (const hipError_t e = lds_opt_in(done, (const void*)kern, (int)lds); e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(rsm::kWaves * 64), lds, stream, (const T*)s, (const T*)q,
+                     (const T*)tab, (T*)out, rows, h, w, hd, scale, bst);
+  return hipGetLastError();
+}
+
+template <typename T, int VB, bool AW>
+static hipError_t pick_items(int items, const void* s, const void* q, const void* tab, void* out, long rows, int h,
+                             int w, int hd, float scale, unsigned blocks, size_t lds, int bst, hipStream_t st) {
+  switch (items) {
+    case 1: return launch_vec<T, VB, 1, AW>(s, q, tab, out, rows, h, w, hd, scale, blocks, lds, bst, st);
+    case 2: return launch_vec<T, VB, 2, AW>(s, q, tab, out, rows, h, w, hd, scale, blocks, lds, bst, st);
+    case 4: return launch_vec<T, VB, 4, AW>(s, q, tab, out, rows, h, w, hd, scale, blocks, lds, bst, st);
+    case 8: return launch_vec<T, VB, 8, AW>(s, q, tab, out, rows, h, w, hd, scale, blocks, lds, bst, st);
+    default:
+      if constexpr (AW) return launch_vec<T, VB, 16, AW>(s, q, tab, out, rows, h, w, hd, scale, blocks, lds, bst, st);
+      return hipErrorInvalidValue;  // not dispatched: such rows take the scalar kernel
+  }
+}
+
+template <typename T>
+static hipError_t launch_relpos_softmax(const void* s, const void* q, const void* tab, void* out, long rows, int h,
+                                        int w, int hd, float scale, hipStream_t stream) {
+  const int n = h * w;
+  const int bst = (h + w + 3) / 4 * 4 + 4;  // 16-byte rows; consecutive rows 4 banks apart for the scatter
+  const long rows_per_block = (long)rsm::kWaves * rsm::kRows;
+  const unsigned blocks = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
+  const size_t lds = (size_t)rsm::kWaves * rsm::kRows * bst * sizeof(float);
+  const long row_bytes = (long)n * (long)sizeof(T);
+  const int vb = row_bytes % 16 == 0 ? 16 : (row_bytes % 8 == 0 ? 8 : 0);
+  if (vb) {
+    const int ve = vb / (int)sizeof(T);
+    const int nvec = n / ve;
+    int items = 1;
+    while (items * 64 < nvec) items *= 2;
+    const bool aw = w % ve == 0 && ve % 4 == 0;  // each vector inside one grid row, whole Rw runs
+    // 16 vectors per lane without whole-row vectors would spill: those rows take the scalar kernel
+    if (items < 16 || (items == 16 && aw)) {
+      if (vb == 16)
+        return aw ? pick_items<T, 16, true>(items, s, q, tab, out, rows, h, w, hd, scale, blocks, lds, bst, stream)
+                  : pick_items<T, 16, false>(items, s, q, tab, out, rows, h, w, hd, scale, blocks, lds, bst, stream);
+      if constexpr ((8 / sizeof(T)) % 4 == 0) {
+        if (aw) return pick_items<T, 8, true>(items, s, q, tab, out, rows, h, w, hd, scale, blocks, lds, bst, stream);
+      }
+      return pick_items<T, 8, false>(items, s, q, tab, out, rows, h, w, hd, scale, blocks, lds, bst, stream);
+    }
+  }
+  auto kern = relpos_softmax_scalar_kernel<T>;
+  static std::atomic<unsigned long long> done{0};
+  if (const hipError_t e = lds_opt_in(done, (const void*)kern, (int)lds); e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(rsm::kWaves * 64), lds, stream, (const T*)s, (const T*)q,
+                     (const T*)tab, (T*)out, rows, h, w, hd, scale, bst);
+  return hipGetLastError();
+}
+
+// Checked by the caller: rows % (h*w) == 0, h*w <= 8192, h, w <= 128, hd <= 256, 16-byte aligned pointers.
 hipError_t relpos_softmax(int dtype, const void* s, const void* q, const void* tab, void* out, long rows, int h, int w,
                           int hd, float scale, hipStream_t stream) {
-  if (dtype == kF32) return pick_items<float>(s, q, tab, out, rows, h, w, hd, scale, stream);
-  if (dtype == kF16) return pick_items<f16>(s, q, tab, out, rows, h, w, hd, scale, stream);
-  return pick_items<bf16>(s, q, tab, out, rows, h, w, hd, scale, stream);
+  if (dtype == kF32) return launch_relpos_softmax<float>(s, q, tab, out, rows, h, w, hd, scale, stream);
+  if (dtype == kF16) return launch_relpos_softmax<f16>(s, q, tab, out, rows, h, w, hd, scale, stream);
+  return launch_relpos_softmax<bf16>(s, q, tab, out, rows, h, w, hd, scale, stream);
 }
 
 }  // namespace samhip

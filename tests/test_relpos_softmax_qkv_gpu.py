@@ -34,9 +34,23 @@ def half_ulp_bf16(x):
     return 2.0 ** (e - 8)
 
 
+# The reference test's geometries, then shapes that take each of the kernel's paths: whole-row
+# 16-byte vectors (64-column grids, and 8192-long rows), 8-byte vectors (14x14 windows in f16), vectors
+# that straddle grid rows (33 and 14 columns), narrow grids (2 columns), the scalar two-pass kernel
+# (odd row lengths, and 8192 f32 columns), and row counts that leave a wave's 32 rows ragged.
+RELPOS_SHAPES = [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (2, 3, 2, 8), (16, 33, 1, 32),
+                 (64, 64, 2, 80), (14, 14, 40, 80), (13, 2, 5, 16), (5, 33, 3, 16), (128, 64, 1, 16),
+                 (91, 90, 1, 8), (1, 64, 7, 24)]
+
+
+LONG_ROWS = {(128, 64, 1, 16), (91, 90, 1, 8)}  # f32 over ~8192 keys: test_relpos_softmax_long_rows_f32
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
-@pytest.mark.parametrize("h,w,bh,hd", [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (2, 3, 2, 8), (16, 33, 1, 32)])
+@pytest.mark.parametrize("h,w,bh,hd", RELPOS_SHAPES)
 def test_relpos_softmax_matches_oracle(hip, h, w, bh, hd, dtype):
+    if dtype == "f32" and (h, w, bh, hd) in LONG_ROWS:
+        pytest.skip("f32 rows of ~8192 keys: checked against the float64 value in test_relpos_softmax_long_rows_f32")
     print(f"relpos_softmax {dtype} {h}x{w} bh={bh} hd={hd}", flush=True)
     n = h * w
     r = np.random.default_rng(h * 100 + w)
@@ -46,6 +60,8 @@ def test_relpos_softmax_matches_oracle(hip, h, w, bh, hd, dtype):
     want = oracle.relpos_softmax(s, q, t, h, w, 0.125)
     got = hip.relpos_softmax(dev(s, dtype), dev(q, dtype), dev(t, dtype), h, w, 0.125)
     got = got.float().cpu().numpy()
+    err = np.abs(got - want).max()
+    print(f"parity relpos_softmax {h}x{w} bh={bh} hd={hd} {dtype}: max-abs {err:.3g}", flush=True)
     if dtype == "f32":
         assert np.abs(got - want).max() / np.abs(want).max() <= 1e-5
     elif dtype == "bf16":
@@ -53,6 +69,40 @@ def test_relpos_softmax_matches_oracle(hip, h, w, bh, hd, dtype):
     else:
         assert np.abs(got - want).max() <= 1e-3
     np.testing.assert_allclose(got.sum(-1), 1.0, atol=2e-2 if dtype == "bf16" else 2e-3)
+
+
+@pytest.mark.parametrize("h,w,bh,hd", sorted(LONG_ROWS))
+def test_relpos_softmax_long_rows_f32(hip, h, w, bh, hd):
+    """f32 rows of 8190 and 8192 keys with the reference test's N(0,1) draws. Over that many keys the
+    reference's own f32 arithmetic (sequential sums, kernels.rs:84-103, which the oracle restates) is
+    1.3e-5 to 1.8e-5 away from the float64 value of the formula on these draws, so the kernel is held to
+    the 1e-5 relative bar against a float64 evaluation on sampled rows; its distance to the oracle is
+    reported beside the oracle's own distance to the float64 value."""
+    n = h * w
+    r = np.random.default_rng(h * 100 + w)
+    s = oracle.round_to(r.standard_normal((bh, n, n)), "f32")
+    q = oracle.round_to(r.standard_normal((bh, n, hd)), "f32")
+    t = oracle.round_to(r.standard_normal((2 * h - 1 + 2 * w - 1, hd)), "f32")
+    got = hip.relpos_softmax(dev(s, "f32"), dev(q, "f32"), dev(t, "f32"), h, w, 0.125).cpu().numpy()[0]
+    want = oracle.relpos_softmax(s, q, t, h, w, 0.125)[0]
+    rows = np.arange(0, n, 61)
+    th, tw = t[:2 * h - 1].astype(np.float64), t[2 * h - 1:].astype(np.float64)
+    exact = []
+    for rr in rows:
+        i, j = rr // w, rr % w
+        qq = q[0, rr].astype(np.float64)
+        rh = np.array([qq @ th[i - kh + h - 1] for kh in range(h)])
+        rw = np.array([qq @ tw[j - kw + w - 1] for kw in range(w)])
+        x = s[0, rr].astype(np.float64) * 0.125 + (rh[:, None] + rw[None, :]).reshape(-1)
+        e = np.exp(x - x.max())
+        exact.append(e / e.sum())
+    exact = np.array(exact)
+    e64 = np.abs(got[rows] - exact).max() / np.abs(exact).max()
+    eor = np.abs(got - want).max() / np.abs(want).max()
+    own = np.abs(want[rows] - exact).max() / np.abs(exact).max()
+    print(f"parity relpos_softmax {h}x{w} f32: vs float64 {e64:.3g}, vs oracle {eor:.3g} (oracle vs float64 "
+          f"{own:.3g})", flush=True)
+    assert e64 <= 1e-5
 
 
 def test_relpos_softmax_rejects_long_rows(hip):
