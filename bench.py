@@ -70,46 +70,81 @@ def window_bytes(bh, n, elem=2, hd=HD):
     return float(bh) * n * hd * elem * 4  # q, kT, v read once, out written once
 
 
-def cpu_baseline():
-    """The oracle (C restatement of the reference's exact-f32 CPU attention, OpenMP on the host
-    threads) on one image's windowed layer and one image's global layer; ms/image = 28 x window +
-    4 x global."""
+def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import numpy as np
-
     import sam_oracle
 
-    cores = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
-    r = np.random.default_rng(1)
+    return sam_oracle
 
-    def time_layer(bh, h, w, reps):
+
+def cpu_cores():
+    return int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        return ""
+
+
+def best_of(fn, reps):
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+    return best
+
+
+def cpu_baseline():
+    """The reference's CPU attention, restated (oracle/), on the host threads, for one image's windowed
+    layer and one image's global layer; ms/image = 28 x window + 4 x global. The reference runs its
+    bf16 branch (TiledAttention with vdpbf16ps GEMMs, kernels.rs:166-179) by default when the CPU has
+    AVX-512 BF16, and its exact-f32 branch (kernels.rs:181-220) otherwise; the default branch is the
+    value, and the f32 branch is reported beside it."""
+    import numpy as np
+
+    sam_oracle = _oracle()
+    cores = cpu_cores()
+    r = np.random.default_rng(1)
+    bf16 = sam_oracle.bf16_available()
+
+    def layer(bh, h, w):
         n = h * w
         q = r.standard_normal((bh, n, HD), dtype=np.float32)
         kt = r.standard_normal((bh, HD, n), dtype=np.float32)
         v = r.standard_normal((bh, n, HD), dtype=np.float32)
         table = (0.02 * r.standard_normal((2 * h - 1 + 2 * w - 1, HD))).astype(np.float32)
-        best = float("inf")
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            sam_oracle.attention_relpos(q, kt, v, table, h, w, HD ** -0.5, nthreads=cores)
-            best = min(best, time.perf_counter() - t0)
-        return best
+        return q, kt, v, table, h, w, HD ** -0.5
 
-    t_win = time_layer(WINDOWS * HEADS, 14, 14, 5)
-    t_glob = time_layer(HEADS, 64, 64, 3)
-    ms = 1e3 * ((DEPTH - len(GLOBAL_LAYERS)) * t_win + len(GLOBAL_LAYERS) * t_glob)
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
-    except OSError:
-        pass
-    return {
-        "value": round(ms, 1), "unit": "ms/image", "cores": cores, "kind": "port",
-        "cpu_model": model, "nproc": os.cpu_count(),
-        "sample": "one windowed layer (400 x 14x14) and one global layer (16 x 64x64) of one image, f32, "
-                  f"best of 5 and 3 runs ({t_win:.3f} s, {t_glob:.3f} s) scaled by 28 and 4 layers",
-    }
+    win, glob = layer(WINDOWS * HEADS, 14, 14), layer(HEADS, 64, 64)
+    nw, ng = DEPTH - len(GLOBAL_LAYERS), len(GLOBAL_LAYERS)
+    t32 = (best_of(lambda: sam_oracle.attention_relpos(*win, nthreads=cores), 3),
+           best_of(lambda: sam_oracle.attention_relpos(*glob, nthreads=cores), 2))
+    ms32 = 1e3 * (nw * t32[0] + ng * t32[1])
+    out = {"unit": "ms/image", "cores": cores, "kind": "port", "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+           "f32_branch_ms": round(ms32, 1)}
+    if bf16:
+        tb = (best_of(lambda: sam_oracle.bf16_attention_relpos(*win, nthreads=cores), 3),
+              best_of(lambda: sam_oracle.bf16_attention_relpos(*glob, nthreads=cores), 2))
+        out.update(value=round(1e3 * (nw * tb[0] + ng * tb[1]), 1), branch="bf16 (the reference's default on "
+                   "AVX-512 BF16 hosts: cpu_gemm.rs PackedB/vdpbf16ps, softmax_row/exp_ps)",
+                   sample=f"one windowed layer (400 x 14x14) and one global layer (16 x 64x64) of one image, best "
+                          f"of 3 and 2 runs (bf16 {tb[0]:.3f} s, {tb[1]:.3f} s; f32 {t32[0]:.3f} s, {t32[1]:.3f} s), "
+                          "scaled by 28 and 4 layers")
+    else:
+        out.update(value=round(ms32, 1), branch="exact f32 (the reference's default without AVX-512 BF16)",
+                   sample=f"one windowed layer (400 x 14x14) and one global layer (16 x 64x64) of one image, f32, "
+                          f"best of 3 and 2 runs ({t32[0]:.3f} s, {t32[1]:.3f} s) scaled by 28 and 4 layers")
+    return out
+
+
+def cpu_leg(seconds, scale, unit_value, unit, sample, kind="port"):
+    """A secondary leg's CPU baseline: `seconds` for the sample, times `scale` to the leg's workload."""
+    return {"value": round(seconds * scale * unit_value, 4), "unit": unit, "cores": cpu_cores(), "kind": kind,
+            "sample": sample}
 
 
 def traffic_from_profiles():
@@ -145,11 +180,19 @@ def check(lib, rc):
         raise RuntimeError(lib.sam_hip_last_error().decode())
 
 
-def secondary(torch, sam_hip, lib, dev, sp, timer):
-    """The other kernels of the path at their workload shapes (synthetic inputs resident in HBM)."""
+def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
+    """The other kernels of the path at their workload shapes (synthetic inputs resident in HBM). With
+    cpu, each leg also carries the reference's CPU path for it (restated in oracle/) timed on a bounded
+    sample on the host threads."""
     res = {}
     g = torch.Generator(device=dev).manual_seed(7)
     vp = ctypes.c_void_p
+    if cpu:
+        import numpy as np
+
+        orc = _oracle()
+        cores = cpu_cores()
+    host = lambda t: t.float().cpu().numpy()
 
     # SAM 2.1 memory attention: per layer self-attention (4096 x 4096) and cross-attention
     # (4096 x 7*4096 + 64 pointer tokens), one head, d 256, 2-D RoPE (theta 1e4) on a 64x64 grid.
@@ -203,6 +246,18 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
                                        4),
         "note": "time includes the key-rotation pass and the key-split combine; flops count attention only",
     }
+    if cpu:
+        # RopeAttn's core on the reference's CPU path (f32 rotation, then sdpa as matmul, softmax, matmul;
+        # sam3/video.rs:106-145, sam3/nn.rs:26-34) for one layer's self and cross attention
+        q0, ks0, vs0, kc0, vc0, _ = layers[0]
+        c0, s0 = host(cos), host(sin)
+        qh, ksh, vsh, kch, vch = (host(t[0, :, 0]) for t in (q0, ks0, vs0, kc0, vc0))
+        ts = best_of(lambda: orc.rope_attention(qh, ksh, vsh, c0, s0, 0, nthreads=cores), 1)
+        tc = best_of(lambda: orc.rope_attention(qh, kch, vch, c0, s0, nptr, nthreads=cores), 1)
+        res["sam2_memory_attention_f16"]["cpu_baseline"] = cpu_leg(
+            ts + tc, 4, 1e3, "ms (4 layers)",
+            f"one layer's self ({ts:.3f} s) and cross ({tc:.3f} s) attention in f32 (the reference's CPU sdpa), "
+            "scaled by 4 layers")
     del layers, ws
 
     # Grounding DINO-tiny deformable attention, f32: 4 levels of an 800x1333 input, 8 heads x 32, 4 points.
@@ -233,6 +288,11 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
+        if cpu:
+            vh, lh, ah = host(value), host(loc), host(attn_w)
+            tcpu = best_of(lambda: orc.deform_attn(vh, lh, ah, shapes, nthreads=cores), 3)
+            res[f"dino_deform_{name}_f32"]["cpu_baseline"] = cpu_leg(
+                tcpu, 1, 1e6, "us", f"the whole layer on cpu::DeformAttn (kernels.rs:776-818), best of 3")
 
         # the same layer through Deform::forward's fused core: offsets, logits and reference points in
         # place of loc and attn (softmax and sampling locations formed in the kernel)
@@ -254,6 +314,12 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
+        if cpu:
+            oh, gh, rh = host(off), host(logits), host(refs)
+            tcpu = best_of(lambda: orc.deform_forward_core(vh, oh, gh, rh, shapes, nthreads=cores), 3)
+            res[f"dino_deform_core_{name}_f32"]["cpu_baseline"] = cpu_leg(
+                tcpu, 1, 1e6, "us", "the whole layer: softmax and sampling locations (dino/mod.rs:166-178), then "
+                                    "cpu::DeformAttn, best of 3")
 
     # relpos_softmax (the reference's GPU step between its two bmm calls) over materialised f16 scores:
     # a ViT-H global layer (16 heads x 4096 rows of 4096) and a windowed layer (400 units x 196 rows of
@@ -278,6 +344,13 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
+        if cpu:
+            part = 1 if name == "global" else 40  # one head of the global layer, 40 of the 400 window units
+            sh_, qh_, th_ = host(sc[:part]), host(qq[:part]), host(tb)
+            tcpu = best_of(lambda: orc.relpos_softmax(sh_, qh_, th_, side, side, HD ** -0.5, nthreads=cores), 2)
+            res[f"vit_h_relpos_softmax_{name}_f16"]["cpu_baseline"] = cpu_leg(
+                tcpu, bh / part, 1e6, "us", f"{part} of the {bh} units on cpu::RelposSoftmax (kernels.rs:62-105, "
+                                            f"f32), best of 2, scaled by {bh // part}")
         del sc, pr
 
     # SAM image preprocessing (image_proc::prepare): a u8 RGB image resized so its longest side is 1024,
@@ -304,6 +377,12 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
                 "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                 "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             }
+            if cpu:
+                ih_ = img.cpu().numpy()
+                tcpu = best_of(lambda: orc.preprocess(ih_, nh, nw, 1024, nthreads=cores), 3)
+                res[f"preprocess_{name}_{dname}"]["cpu_baseline"] = cpu_leg(
+                    tcpu, 1, 1e6, "us", "the whole image on image_proc::resize_normalize (image_proc.rs:57-96, f32), "
+                                        "best of 3")
 
     # The encoder attention sweep (ViT-B / ViT-L / ViT-H, f16, batch 1, 4 and 8): every attention layer of
     # the encoder on fresh q/kT/v per layer, back to back, in ms per image. Windowed layers are
@@ -340,6 +419,30 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
                 "window_layer_us": round(layer_us[14][0], 2), "global_layer_us": round(layer_us[64][0], 2),
                 "tflops": round(gf / total_ms, 1),
             }
+        if cpu:
+            # the reference's default CPU attention (bf16 branch on AVX-512 BF16 hosts, else exact f32) per
+            # image: 5 of the 25 windows and 2 of the heads of a global layer, scaled up (the CPU cost is
+            # linear in units and in batch)
+            fn = orc.bf16_attention_relpos if orc.bf16_available() else orc.attention_relpos
+            rr = np.random.default_rng(3)
+
+            def units(bh, side):
+                n = side * side
+                return (rr.standard_normal((bh, n, hd), dtype=np.float32),
+                        rr.standard_normal((bh, hd, n), dtype=np.float32),
+                        rr.standard_normal((bh, n, hd), dtype=np.float32),
+                        (0.02 * rr.standard_normal((4 * side - 2, hd))).astype(np.float32))
+
+            wu, gu = units(5 * heads, 14), units(2, 64)
+            tw = best_of(lambda: fn(*wu, 14, 14, hd ** -0.5, nthreads=cores), 2)
+            tg = best_of(lambda: fn(*gu, 64, 64, hd ** -0.5, nthreads=cores), 2)
+            ng_ = len(glob)
+            leg = cpu_leg(1.0, 1.0, 1e3 * ((depth - ng_) * tw * 5 + ng_ * tg * heads / 2), "ms/image",
+                          f"{'bf16' if orc.bf16_available() else 'exact f32'} branch of the reference's CPU attention: "
+                          f"5 of 25 windows x {heads} heads ({tw:.3f} s) and 2 of {heads} global heads ({tg:.3f} s), "
+                          f"scaled to {depth - ng_} windowed and {ng_} global layers")
+            for batch in (1, 4, 8):
+                res[f"sweep_{mname}_attention_b{batch}_f16"]["cpu_baseline"] = leg
 
     # Encoder-level timing: the whole SAM image encoder (patch embedding, all blocks with their qkv / proj
     # / MLP linears on hipBLASLt through torch, LayerNorms, the neck) on this library's attention,
@@ -380,6 +483,11 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
+        if cpu:
+            yh, bh_ = host(y), host(bq)
+            tcpu = best_of(lambda: orc.qkv_split(yh, bh_, n, 16, 80, nthreads=cores), 3)
+            res[f"vit_h_qkv_split_{name}_f16"]["cpu_baseline"] = cpu_leg(
+                tcpu, 1, 1e6, "us", "the whole block on cpu::QkvSplit (kernels.rs:239-263, f32), best of 3")
 
     # The elementwise steps beside attention in a ViT-H block, f16: the projection output plus bias plus
     # the residual (4096 tokens x 1280), and the MLP's bias + exact GELU (4096 x 5120).
@@ -405,6 +513,14 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
+        if cpu:
+            yh, rh_, bh_ = host(y), host(resid), host(bvec)
+            f = (lambda: orc.bias_residual(rh_, yh, bh_)) if name == "bias_residual" else (lambda: orc.bias_gelu(yh, bh_))
+            tcpu = best_of(f, 2)
+            res[f"vit_h_{name}_f16"]["cpu_baseline"] = cpu_leg(
+                tcpu, 1, 1e6, "us", f"the whole tensor on cpu::{'BiasResidual' if name == 'bias_residual' else 'BiasGelu'} "
+                                    "(kernels.rs:618-663, f32, one thread), best of 2", kind="port")
+            res[f"vit_h_{name}_f16"]["cpu_baseline"]["cores"] = 1
 
     # SAM ViT-B encoder attention layers, f32 (12 heads x 64): window 300 x 14x14, global 12 x 64x64.
     for name, bh, hw in (("window", 300, 14), ("global", 12, 64)):
@@ -426,6 +542,12 @@ def secondary(torch, sam_hip, lib, dev, sp, timer):
             "us": round(ms * 1e3, 2), "tflops": round(f / (ms * 1e-3) / 1e12, 2),
             "frac_of_f32_peak": round(f / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f32"], 4),
         }
+        if cpu:
+            arr = [host(t) for t in (q, kt, v, table)]
+            tcpu = best_of(lambda: orc.attention_relpos(*arr, hw, hw, 0.125, nthreads=cores), 2)
+            res[f"vit_b_{name}_f32"]["cpu_baseline"] = cpu_leg(
+                tcpu, 1, 1e6, "us", "the whole layer on the reference's exact-f32 TiledAttention branch "
+                                    "(kernels.rs:181-220), best of 2")
     return res
 
 
@@ -568,7 +690,7 @@ def main():
         "encoder_tflops": round(total_flops / (ms_step * 1e-3) / 1e12, 1),
     }
     if not args.no_secondary:
-        line["secondary"] = secondary(torch, sam_hip, lib, dev, sp, Timer(torch, stream))
+        line["secondary"] = secondary(torch, sam_hip, lib, dev, sp, Timer(torch, stream), cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

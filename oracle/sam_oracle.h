@@ -6,7 +6,8 @@
  * benchmark load it, and never as the thing that is measured or shipped. The product path
  * (libsam_hip.so) does not link, call or fall back to anything here.
  *
- * All arrays are contiguous, row-major f32 (the reference CPU path is f32-only). `nthreads` <= 0
+ * All arrays are contiguous, row-major f32 (the reference's CPU ops take f32; its bf16 path rounds
+ * operands to bf16 inside its GEMMs, restated in oracle_bf16.c). `nthreads` <= 0
  * means "all OpenMP threads". Every function cites the reference lines it restates.
  *
  * Parity pins (see tests/test_oracle.py): each function is checked against an independent float64
@@ -16,6 +17,8 @@
  */
 #ifndef SAM_ORACLE_H
 #define SAM_ORACLE_H
+
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -90,4 +93,15 @@ void oracle_randn(unsigned long long seed, float* out, long n, float mean, float
 #ifdef __cplusplus
 }
 #endif
+/* The reference's default CPU path on AVX-512 BF16 machines (cpu_gemm.rs, kernels.rs:139-179), in
+ * oracle_bf16.c. Call only when oracle_bf16_available() is nonzero. */
+int oracle_bf16_available(void);
+void oracle_bf16_round(const float* x, uint16_t* out, long n);
+void oracle_bf16_exp(const float* x, float* y, long n);
+void oracle_bf16_matmul(const float* x, const float* w, float* c, int m, int k, int n, int nthreads);
+void oracle_bf16_attention_relpos(const float* q, const float* kt, const float* v, const float* table, float* out,
+                                  long bh, int h, int w, int hd, float scale, int nthreads);
+void oracle_bf16_flash_attention(const float* q, const float* k, const float* v, float* out, int b, int lq, int lk,
+                                 int h, int d, float scale, int nthreads);
+
 #endif

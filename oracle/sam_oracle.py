@@ -51,6 +51,14 @@ def lib():
         L.oracle_preprocess.argtypes = [ctypes.c_void_p] + [ctypes.c_int] * 5 + [_F, _F, _F, ctypes.c_int]
         L.oracle_bias_residual.argtypes = [_F, _F, _F, _F, ctypes.c_long, ctypes.c_int]
         L.oracle_bias_gelu.argtypes = [_F, _F, _F, ctypes.c_long, ctypes.c_int]
+        L.oracle_bf16_available.restype = ctypes.c_int
+        _U16 = ctypes.POINTER(ctypes.c_uint16)
+        L.oracle_bf16_round.argtypes = [_F, _U16, ctypes.c_long]
+        L.oracle_bf16_exp.argtypes = [_F, _F, ctypes.c_long]
+        L.oracle_bf16_matmul.argtypes = [_F, _F, _F] + [ctypes.c_int] * 4
+        L.oracle_bf16_attention_relpos.argtypes = [_F] * 5 + [ctypes.c_long] + [ctypes.c_int] * 3 + [ctypes.c_float,
+                                                                                                   ctypes.c_int]
+        L.oracle_bf16_flash_attention.argtypes = [_F] * 4 + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int]
         L.oracle_round_f16.argtypes = [_F, ctypes.c_long]
         L.oracle_round_bf16.argtypes = [_F, ctypes.c_long]
         L.oracle_randn.argtypes = [ctypes.c_ulonglong, _F, ctypes.c_long, ctypes.c_float, ctypes.c_float]
@@ -131,6 +139,70 @@ def deform_forward_core(value, off, logits, refs, shapes, nthreads: int = 0) -> 
     """Deform::forward between its projections (dino/mod.rs:166-179): deform_prep, then deform_attn."""
     loc, attn = deform_prep(off, logits, refs, shapes, nthreads)
     return deform_attn(value, loc, attn, shapes, nthreads)
+
+
+def bf16_available() -> bool:
+    """Whether this CPU has AVX-512F and AVX-512 BF16, the condition for the reference's bf16 CPU path
+    (cpu_gemm.rs:14-32)."""
+    return bool(lib().oracle_bf16_available())
+
+
+def _need_bf16():
+    if not bf16_available():
+        raise RuntimeError("the bf16 CPU path needs AVX-512 BF16 (cpu_gemm.rs:14-24)")
+
+
+def bf16_bits(x) -> np.ndarray:
+    """cpu_gemm.rs:38-45: f32 -> bf16 bits (round to nearest even)."""
+    x = _f32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().oracle_bf16_round(_p(x), out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), x.size)
+    return out
+
+
+def bf16_exp(x) -> np.ndarray:
+    """cpu_gemm.rs:272-286 (exp_ps) elementwise."""
+    _need_bf16()
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().oracle_bf16_exp(_p(x), _p(y), x.size)
+    return y
+
+
+def bf16_matmul(x, w, nthreads: int = 0) -> np.ndarray:
+    """cpu_gemm.rs:100-178: x [M, K] @ w [K, N] with bf16 operands and f32 accumulation (vdpbf16ps)."""
+    _need_bf16()
+    x, w = _f32(x), _f32(w)
+    m, k = x.shape
+    k2, n = w.shape
+    assert k == k2
+    c = np.empty((m, n), np.float32)
+    lib().oracle_bf16_matmul(_p(x), _p(w), _p(c), m, k, n, nthreads)
+    return c
+
+
+def bf16_attention_relpos(q, kt, v, table, h: int, w: int, scale: float, nthreads: int = 0) -> np.ndarray:
+    """kernels.rs:139-179 (TiledAttention, bf16 branch): the reference's default CPU attention."""
+    _need_bf16()
+    q, kt, v, table = _f32(q), _f32(kt), _f32(v), _f32(table)
+    bh, n, hd = q.shape
+    assert n == h * w and kt.shape == (bh, hd, n) and v.shape == (bh, n, hd)
+    out = np.empty_like(q)
+    lib().oracle_bf16_attention_relpos(_p(q), _p(kt), _p(v), _p(table), _p(out), bh, h, w, hd, scale, nthreads)
+    return out
+
+
+def bf16_flash_attention(q, k, v, scale: float | None = None, nthreads: int = 0) -> np.ndarray:
+    """cpu_gemm.rs:361-417: q [B, Lq, H, D], k/v [B, Lk, H, D] -> [B, Lq, H, D] on the bf16 kernels."""
+    _need_bf16()
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    b, lq, h, d = q.shape
+    lk = k.shape[1]
+    assert k.shape == (b, lk, h, d) and v.shape == k.shape
+    scale = d ** -0.5 if scale is None else scale
+    out = np.empty_like(q)
+    lib().oracle_bf16_flash_attention(_p(q), _p(k), _p(v), _p(out), b, lq, lk, h, d, scale, nthreads)
+    return out
 
 
 def sdpa(q, k, v, nthreads: int = 0) -> np.ndarray:

@@ -495,3 +495,140 @@ def test_bias_gelu_matches_float64_erf_and_its_limits(oracle_lib):
     big = np.array([[0.0, 12.0, -12.0, 1e-30]], np.float32)
     out = oracle_lib.bias_gelu(big, np.zeros(4, np.float32))
     assert out[0, 0] == 0.0 and out[0, 1] == 12.0 and out[0, 2] == 0.0 and out[0, 3] == np.float32(5e-31)
+
+
+# ------------------------------------------------------------------ bf16 CPU path (cpu_gemm.rs)
+
+bf16_cpu = pytest.mark.skipif("not __import__('sam_oracle').bf16_available()",
+                              reason="the reference's bf16 CPU path needs AVX-512 BF16 (cpu_gemm.rs:14-24)")
+
+
+def test_bf16_bits_round_to_nearest_even(oracle_lib):
+    """cpu_gemm.rs:38-45 against torch's f32 -> bfloat16 conversion (round to nearest even), including
+    exact halfway cases in both directions."""
+    import torch
+
+    r = _rng(61)
+    x = np.concatenate([r.standard_normal(5000), r.standard_normal(1000) * 1e30, r.standard_normal(1000) * 1e-30])
+    halves = np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x3F80C000, 0x7F7F8000], np.uint32).view(np.float32)
+    x = np.concatenate([x.astype(np.float32), halves, np.float32([0.0, -0.0, np.inf, -np.inf])])
+    got = oracle_lib.bf16_bits(x)
+    want = torch.from_numpy(x).bfloat16().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def _vdpbf16_emulation(a, w):
+    """a [m, k] @ w [k, n] as the bf16 microkernel computes it, in numpy float32 from the instruction's
+    definition: operands rounded to bf16; per output, for each k pair (2q, 2q+1) in order,
+    acc = (acc + a[2q+1] w[2q+1]) + a[2q] w[2q], each product exact in f32, each sum rounded."""
+    import torch
+
+    ab = torch.from_numpy(a).bfloat16().float().numpy()
+    wb = torch.from_numpy(w).bfloat16().float().numpy()
+    m, k = a.shape
+    n = w.shape[1]
+    if k % 2:
+        ab = np.concatenate([ab, np.zeros((m, 1), np.float32)], 1)
+        wb = np.concatenate([wb, np.zeros((1, n), np.float32)], 0)
+    acc = np.zeros((m, n), np.float32)
+    for q in range(ab.shape[1] // 2):
+        acc = (acc + np.outer(ab[:, 2 * q + 1], wb[2 * q + 1]).astype(np.float32)).astype(np.float32)
+        acc = (acc + np.outer(ab[:, 2 * q], wb[2 * q]).astype(np.float32)).astype(np.float32)
+    return acc
+
+
+@bf16_cpu
+@pytest.mark.parametrize("m,k,n", [(11, 27, 45), (70, 80, 33), (8, 16, 32), (1, 1, 1), (130, 33, 70)])
+def test_bf16_matmul_is_the_vdpbf16ps_sequence(oracle_lib, m, k, n):
+    """The packed bf16 GEMM (odd sizes: partial panels, odd K, partial row blocks) equals, bit for bit,
+    an emulation of the instruction sequence written from its definition."""
+    r = _rng(62 + m + k + n)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    w = r.standard_normal((k, n)).astype(np.float32)
+    assert np.array_equal(oracle_lib.bf16_matmul(a, w), _vdpbf16_emulation(a, w))
+
+
+@bf16_cpu
+def test_bf16_matmul_reference_bar(oracle_lib):
+    """tests/cpu_gemm.rs:11-27: |bf16 matmul - f32 matmul| < 4e-3 of |x| |w| (Frobenius)."""
+    r = _rng(63)
+    x = r.standard_normal((37, 300)).astype(np.float32)
+    w = r.standard_normal((300, 51)).astype(np.float32)
+    err = np.abs(oracle_lib.bf16_matmul(x, w) - x.astype(np.float64) @ w).max()
+    assert err < 4e-3 * np.linalg.norm(x) * np.linalg.norm(w) / np.sqrt(x.shape[0] * w.shape[1])
+
+
+@bf16_cpu
+def test_bf16_exp_accuracy_and_clamp(oracle_lib):
+    """cpu_gemm.rs:272-286: relative error about 1e-7 near 0, plus the f32 rounding of t = x log2(e): the
+    product's rounding (at most |t| 2^-24) and the constant's (|t| 2^-25), times ln 2, so at most
+    1.04 |t| 2^-24 (checked point by point against float64 exp: below 2e-7 + 1.1 |t| 2^-24); exp(0) = 1
+    exactly; below -126 ln 2 the argument clamps to 2^-126."""
+    x = np.concatenate([np.linspace(-87.0, 0.0, 200001), -np.logspace(-8, 1.9, 1000)]).astype(np.float32)
+    y = oracle_lib.bf16_exp(x)
+    rel = np.abs(y.astype(np.float64) / np.exp(x.astype(np.float64)) - 1.0)
+    t = np.abs(x.astype(np.float64)) * np.log2(np.e)
+    assert (rel <= 2e-7 + 1.1 * t * 2.0 ** -24).all()
+    assert oracle_lib.bf16_exp(np.float32([0.0]))[0] == 1.0
+    assert oracle_lib.bf16_exp(np.float32([-200.0, -1000.0]))[0] == np.float32(2.0 ** -126)
+
+
+@bf16_cpu
+@pytest.mark.parametrize("h,w,bh,hd", [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80)])
+def test_bf16_attention_relpos_reference_bar(oracle_lib, h, w, bh, hd):
+    """tests/cpu_gemm.rs:30-50: attention_relpos_cpu with bf16 on vs off over the reference test's three
+    geometries, mean relative error < 1.5e-2 (N(0,1) inputs, scale 0.125)."""
+    r = _rng(64 + h * w)
+    n = h * w
+    q = r.standard_normal((bh, n, hd)).astype(np.float32)
+    kt = r.standard_normal((bh, hd, n)).astype(np.float32)
+    v = r.standard_normal((bh, n, hd)).astype(np.float32)
+    t = r.standard_normal((2 * h - 1 + 2 * w - 1, hd)).astype(np.float32)
+    got = oracle_lib.bf16_attention_relpos(q, kt, v, t, h, w, 0.125)
+    want = oracle_lib.attention_relpos(q, kt, v, t, h, w, 0.125)
+    rel = np.abs(got - want).mean() / np.abs(want).mean()
+    assert rel < 1.5e-2
+
+
+@bf16_cpu
+def test_bf16_attention_relpos_rounding_points(oracle_lib):
+    """The bf16 branch rounds q, kT (for the score GEMM) and P, v (for the output GEMM) to bf16, and keeps
+    the rel-pos dot products, the softmax and the accumulations in f32: a float64 model with exactly
+    those roundings is within 1e-3, a model that skips the rounding of P is not."""
+    import torch
+
+    h, w, bh, hd = 7, 11, 2, 80
+    r = _rng(65)
+    n = h * w
+    q = r.standard_normal((bh, n, hd)).astype(np.float32)
+    kt = r.standard_normal((bh, hd, n)).astype(np.float32)
+    v = r.standard_normal((bh, n, hd)).astype(np.float32)
+    t = (0.5 * r.standard_normal((2 * h - 1 + 2 * w - 1, hd))).astype(np.float32)
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).bfloat16().double().numpy()
+    got = oracle_lib.bf16_attention_relpos(q, kt, v, t, h, w, 0.125)
+    s = bf(q) @ bf(kt)
+    bias = refimpl.relpos_logits64(np.zeros_like(s), q, t, h, w, 0.125)
+    p = refimpl.softmax64(0.125 * s + bias)
+    with_round = bf(p) @ bf(v)
+    without = p @ bf(v)
+    e1, e2 = np.abs(got - with_round).max(), np.abs(got - without).max()
+    assert e1 < 1e-3 < e2, (e1, e2)
+
+
+@bf16_cpu
+def test_bf16_flash_attention(oracle_lib):
+    """cpu_gemm.rs:361-417: against the exact attention (the reference's bf16-vs-f32 bar, mean relative
+    < 1.5e-2), and with a single key every query returns that key's value rounded to bf16."""
+    import torch
+
+    r = _rng(66)
+    b, lq, lk, h, d = 2, 45, 70, 3, 64
+    q = r.standard_normal((b, lq, h, d)).astype(np.float32)
+    k = r.standard_normal((b, lk, h, d)).astype(np.float32)
+    v = r.standard_normal((b, lk, h, d)).astype(np.float32)
+    got = oracle_lib.bf16_flash_attention(q, k, v)
+    want = oracle_lib.mha_blhd(q, k, v)
+    assert np.abs(got - want).mean() / np.abs(want).mean() < 1.5e-2
+    one = oracle_lib.bf16_flash_attention(q, k[:, :1], v[:, :1])
+    vb = torch.from_numpy(v[:, :1]).bfloat16().float().numpy()
+    assert np.array_equal(one, np.broadcast_to(vb, one.shape))
