@@ -291,6 +291,13 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
         s[mb] = mma32(a, qf[k], k == 0 ? cinit[mb] : s[mb]);
       }
     }
+    // the transpose reads run three MFMAs ahead, so that the LDS latency hides behind the MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+    for (int i = 0; i < 2 * kKS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
   };
   // f16: + (Rh - m_run) of tile t through the extra k-step, once m_run is known
   auto qk_b = [&](int t, f32x16* s) {
@@ -384,6 +391,14 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
         o[ob] = mma32(a, b[w4], o[ob]);
         if (kSplitP) o[ob] = mma32(a, blo[w4], o[ob]);
       }
+    if constexpr (!kSplitP) {  // reads three MFMAs ahead, as in qk_k
+      __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+      for (int i = 0; i < 4 * kMBO; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+    }
   };
 
   f32x16 sa[2], sb[2];

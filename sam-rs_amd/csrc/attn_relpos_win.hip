@@ -26,10 +26,13 @@
 //     memory operations complete in issue order), then one barrier publishes everyone's share;
 //   * kT tiles are stored [d][64 slots] with the 8-byte chunks of each row XOR-swizzled by the row's
 //     low bits, so the transpose reads (ds_read_b64_tr_b16) of four consecutive rows hit disjoint
-//     banks; V tiles are [64 slots][hd]. hd 80: the O^T rows 80..95 read past a slot's 80 columns and
-//     are discarded. hd 64: the 8-byte chunks of slots 2, 3 (mod 4) are rotated by 8, so the transpose
-//     reads of four consecutive slots at a 128-byte pitch hit disjoint banks. The softmax denominator
-//     is summed on the VALU.
+//     banks; V tiles are [64 slots][hd] with the 8-byte chunks of a slot rotated: hd 80 (160-byte
+//     pitch) moves even slots by 4 chunks, hd 64 (128-byte pitch) slots 2, 3 (mod 4) by 8, so that the
+//     4 slots x 8 chunks of a half wave's transpose read fall on 64 distinct banks. hd 80: the O^T rows
+//     80..95 are discarded (their lanes re-read block 0). The softmax denominator is summed on the VALU;
+//   * q rows and table rows are [row][hd] with the 16-byte chunks of a row rotated (hd 80: by one for
+//     rows 8..15 of every 16; hd 64: by (row / 2) mod 8), so that the 16-byte reads of 16 rows at one
+//     column fall on 64 distinct banks.
 // Padding keys (columns >= W, rows >= H) and padding table rows read valid data of the same tensor:
 // the keys' bias is -inf (P = 0), and the table rows' products are never scattered.
 // Limits (checked by the dispatcher): 13 <= H <= 16 (4 key tiles), W <= 16 and even, hd 80 or 64,
@@ -61,22 +64,24 @@ template <int HD> struct Shape {
   static constexpr int kTDma = kKDma + kVDma;    // DMAs per wave per tile
   static constexpr int kQDma = kQRows * HD * 2 / 1024 / kWaves;  // 1 KB units of q per wave: 5 or 4
   static constexpr int kChunks = HD / 4;         // 8-byte chunks of a V slot
-  // Buffer b is a kT tile at 2 b kTile and a V tile right after it; the last V tile is followed by 16
-  // spare elements for the discarded O^T rows of its last slot (hd 80). The q rows fill buffer 1 and
+  static constexpr int kQChunks = HD / 8;        // 16-byte chunks of a q or table row
+  // Buffer b is a kT tile at 2 b kTile and a V tile right after it. The q rows fill buffer 1 and
   // the table the kT half of buffer 2 until the prologue has read them; a wave's bias scratch then
   // overlays its own 32 q rows, which it alone reads (into registers) before it scatters.
   static constexpr int kBuf = 2 * kTile;
   static constexpr int kQOff = kBuf;
   static constexpr int kTbOff = 2 * kBuf;
-  static constexpr size_t kLdsBytes = (size_t)(kRing * kBuf + 16) * 2;
+  static constexpr size_t kLdsBytes = (size_t)kRing * kBuf * 2;
   static_assert(HD == 80 || HD == 64, "head dims");
   static_assert(kRhsRows * 32 * sizeof(float) <= 32 * HD * 2, "the scratch fits in a wave's q rows");
   static_assert((HD == 64 ? 3 : 2) * kLdsBytes <= 160 * 1024, "workgroups per CU");
   static_assert(kQRows * HD * 2 % (1024 * kWaves) == 0, "DMA split");
   static_assert(kTile * 2 <= kKDma * kWaves * 1024 && kTRows * HD * 2 <= kTbDma * kWaves * 1024, "units");
   static_assert(kQRows * HD <= kBuf && kTRows * HD <= kTile, "staging fits buffers 1 and 2");
-  // V chunk rotation: chunk c of slot r is stored at (c + vrot(r)) % kChunks
-  static constexpr int vrot(int r) { return HD == 64 && ((r >> 1) & 1) ? 8 : 0; }
+  // V chunk rotation: 8-byte chunk c of slot r is stored at (c + vrot(r)) % kChunks
+  static constexpr int vrot(int r) { return HD == 80 ? ((r & 1) ? 0 : 4) : (((r >> 1) & 1) ? 8 : 0); }
+  // q / table row rotation: 16-byte chunk c of LDS row r is stored at (c + qrot(r)) % kQChunks
+  static constexpr int qrot(int r) { return HD == 80 ? ((r >> 3) & 1) : ((r >> 1) & 7); }
   // DMA unit of part i0 (parts past the last unit repeat the first ones)
   static constexpr int unit(int i0) { return i0 < kUnits ? i0 : i0 - kUnits; }
 };
@@ -173,7 +178,8 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
     for (int p = 0; p < S::kQDma; ++p) {
       const int i = wave * S::kQDma + p;  // unit i covers q-image elements [512 i, 512 i + 512)
       const int e = i * 512 + 8 * lane;
-      const int row = e / HD, col = e % HD;
+      const int row = e / HD, ch = (e % HD) >> 3;
+      const int col = 8 * ((ch + S::kQChunks - S::qrot(row)) % S::kQChunks);
       const int src = q0 + row;  // queries past the end read query 0
       dma16(base, (unsigned)(sizeof(T) * ((src < N ? src : 0) * HD + col)), lds0 + (S::kQOff + i * 512) * 2);
     }
@@ -186,7 +192,8 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
     for (int p = 0; p < S::kTbDma; ++p) {
       const int i = S::unit(wave + kWaves * p);
       const int e = i * 512 + 8 * lane;
-      const int r = e / HD, col = e % HD;
+      const int r = e / HD, ch = (e % HD) >> 3;
+      const int col = 8 * ((ch + S::kQChunks - S::qrot(r)) % S::kQChunks);
       const int src = r < 32 ? (r < 2 * H - 1 ? r : 0) : (r - 32 < 2 * W - 1 ? 2 * H - 1 + r - 32 : 0);
       dma16(base, (unsigned)(sizeof(T) * (src * HD + col)), lds0 + (S::kTbOff + i * 512) * 2);
     }
@@ -204,9 +211,11 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
     koff[mb] = d * 64 + (((slot >> 2) ^ kswz(d & 3)) << 2);
   }
   // V^T (A operand of O^T): source lane (4*s + c) reads the slot of key 16*(w4&1) + 8*r + 4*(g>>1) + s of
-  // block w4>>1, columns 32*ob + 16*(g&1) + 4*c .. +3 (logical chunk 8*ob + 4*(g&1) + c). hd 80 has no
-  // rotation, so block ob is 32 columns further; hd 64 keeps an offset per block (the rotation wraps).
-  constexpr int kVB = HD == 80 ? 1 : kMBO;
+  // block w4>>1, columns 32*ob + 16*(g&1) + 4*c .. +3 (logical chunk 8*ob + 4*(g&1) + c). hd 80: block
+  // 1 is 8 chunks after block 0 (no wrap: c + vrot <= 11); block 2 has its own offsets (the rotation
+  // wraps), and its lanes of the discarded rows 80..95 read what the data lanes 16 below them read, so
+  // the half wave touches no further banks; hd 64 keeps an offset per block.
+  constexpr int kVB = HD == 80 ? 2 : kMBO;
   int voff[kVB][4][2];
 #pragma unroll
   for (int ob = 0; ob < kVB; ++ob)
@@ -216,7 +225,7 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
       for (int r = 0; r < 2; ++r) {
         const int ms = 16 * (w4 & 1) + 8 * r + 4 * (g >> 1) + (gi >> 2);
         const int slot = KG::slot(w4 >> 1, ms);
-        const int c = 8 * ob + 4 * (g & 1) + (gi & 3);
+        const int c = HD == 80 && ob == 1 ? 16 + (gi & 3) : 8 * ob + 4 * (g & 1) + (gi & 3);
         voff[ob][w4][r] = slot * HD + 4 * ((c + S::vrot(slot)) % S::kChunks);
       }
   auto wave_sync = [&]() {
@@ -232,15 +241,17 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   X8 qf[kKS];
 #pragma unroll
   for (int s = 0; s < kKS; ++s)
-    qf[s] = *reinterpret_cast<const X8*>(kring + S::kQOff + (wave * 32 + n) * HD + 16 * s + 8 * hh);
+    qf[s] = *reinterpret_cast<const X8*>(kring + S::kQOff + (wave * 32 + n) * HD +
+                                         8 * ((2 * s + hh + S::qrot(n)) % S::kQChunks));
   f32x16 cinit;
   float rh[kTiles][2];
   {
     f32x16 gh = f32x16{}, gw = f32x16{};
 #pragma unroll
     for (int s = 0; s < kKS; ++s) {
-      const X8 ah = *reinterpret_cast<const X8*>(tb + n * HD + 16 * s + 8 * hh);
-      const X8 aw = *reinterpret_cast<const X8*>(tb + (32 + n) * HD + 16 * s + 8 * hh);
+      const int col = 8 * ((2 * s + hh + S::qrot(n)) % S::kQChunks);  // rows n and 32 + n rotate alike
+      const X8 ah = *reinterpret_cast<const X8*>(tb + n * HD + col);
+      const X8 aw = *reinterpret_cast<const X8*>(tb + (32 + n) * HD + col);
       gh = mma32(ah, qf[s], gh);
       gw = mma32(aw, qf[s], gw);
     }
@@ -352,7 +363,7 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
     for (int w4 = 0; w4 < 2 * NB; ++w4) {
 #pragma unroll
       for (int ob = 0; ob < kMBO; ++ob) {
-        const int vo = HD == 80 ? 32 * ob : 0, vb = HD == 80 ? 0 : ob;
+        const int vo = HD == 80 && ob == 1 ? 32 : 0, vb = HD == 80 ? ob >> 1 : ob;
         const X8 a = join8<T>(lds_read_tr16(vbuf + voff[vb][w4][0] + vo), lds_read_tr16(vbuf + voff[vb][w4][1] + vo));
         o[ob] = mma32(a, b[w4], o[ob]);
         if (kSplitP) o[ob] = mma32(a, blo[w4], o[ob]);
