@@ -19,9 +19,9 @@
 // a tile exceeds it by more than 8 (log2 units), so the O rescale is skipped on almost every tile.
 //
 // Few query blocks (SAM 2 memory attention: one head, 4096 queries, 4096 or 28736 keys) would leave
-// most of the 256 CUs idle, so the keys are split across workgroups; each split writes an unnormalised
-// f32 partial O with its running max and sum, and flash_combine_kernel merges the splits by
-// log-sum-exp. Workgroups are numbered XCD-major with all query blocks of one (head, split) adjacent,
+// most of the 256 CUs idle, so the keys are split across workgroups; each split writes a partial O
+// (f16: normalised by its own sum, in f16, half the bytes of f32; bf16: unnormalised, in f32) with its
+// running max and sum, and flash_combine_kernel merges the splits by log-sum-exp. Workgroups are numbered XCD-major with all query blocks of one (head, split) adjacent,
 // so the K/V range of a split is fetched into one XCD's L2 and shared there.
 //
 // Optional RoPE on the queries (the first n_rope_q rows, table row = query % rope_rows) is applied while
@@ -321,19 +321,35 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
         }
       }
   } else {
-    // unnormalised partial O [split][bh][q][DP] (f32) and (max, sum) [split][bh][q][2]
+    // partial O [split][bh][q][DP] and (max, sum) [split][bh][q][2]: f16 stores O / sum (a convex
+    // combination of f16 values of v, so it stays in range), bf16 the unnormalised O in f32
     const long row = ((long)split * p.b * p.h + bhi) * p.lq + qidx;
-    float* prow = p.opart + row * DP;
+    if constexpr (__is_same(T, f16)) {
+      const float inv = 1.f / l;
+      f16* prow = reinterpret_cast<f16*>(p.opart) + row * DP;
 #pragma unroll
-    for (int ob = 0; ob < MBO; ++ob)
+      for (int ob = 0; ob < MBO; ++ob)
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int d0 = 32 * ob + 8 * a + 4 * hh;
-        f32x4 w4;
+        for (int a = 0; a < 4; ++a) {
+          const int d0 = 32 * ob + 8 * a + 4 * hh;
+          Vec<f16>::x4 w4;
 #pragma unroll
-        for (int bb = 0; bb < 4; ++bb) w4[bb] = o[ob][4 * a + bb];
-        *reinterpret_cast<f32x4*>(prow + d0) = w4;
-      }
+          for (int bb = 0; bb < 4; ++bb) w4[bb] = (f16)(o[ob][4 * a + bb] * inv);
+          *reinterpret_cast<Vec<f16>::x4*>(prow + d0) = w4;
+        }
+    } else {
+      float* prow = p.opart + row * DP;
+#pragma unroll
+      for (int ob = 0; ob < MBO; ++ob)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const int d0 = 32 * ob + 8 * a + 4 * hh;
+          f32x4 w4;
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb) w4[bb] = o[ob][4 * a + bb];
+          *reinterpret_cast<f32x4*>(prow + d0) = w4;
+        }
+    }
     if (hh == 0) {
       float2 ml;
       ml.x = m_run;
@@ -343,8 +359,9 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
   }
 }
 
-// out[b, q, h, :] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, M = max_s m_s. One wave per row,
-// each lane 4 consecutive columns.
+// out[b, q, h, :] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, M = max_s m_s, with O_s the
+// unnormalised partial (bf16: f32 partials) or l_s times the stored O_s / l_s (f16: f16 partials). One
+// wave per row, each lane 4 consecutive columns.
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p) {
   const int lane = threadIdx.x & 63;
@@ -359,8 +376,18 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p) {
   const int c = 4 * lane;
   for (int s = 0; s < p.nsplit; ++s) {
     const float w = exp2_fast(p.ml[(s * plane + row) * 2] - mx);
-    den += w * p.ml[(s * plane + row) * 2 + 1];
-    if (c < DP) acc += w * *reinterpret_cast<const f32x4*>(p.opart + (s * plane + row) * DP + c);
+    const float wl = w * p.ml[(s * plane + row) * 2 + 1];
+    den += wl;
+    if (c < DP) {
+      if constexpr (__is_same(T, f16)) {
+        const Vec<f16>::x4 o4 = *reinterpret_cast<const Vec<f16>::x4*>(reinterpret_cast<const f16*>(p.opart) +
+                                                                      (s * plane + row) * DP + c);
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) acc[bb] += wl * (float)o4[bb];
+      } else {
+        acc += w * *reinterpret_cast<const f32x4*>(p.opart + (s * plane + row) * DP + c);
+      }
+    }
   }
   if (c >= p.d) return;
   const float inv = 1.f / den;

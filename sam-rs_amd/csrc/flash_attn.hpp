@@ -15,7 +15,7 @@ struct FlashParams {
   int b, h, lq, lk, d;
   float sc;                    // scale * log2(e)
   int qblocks, nsplit, tps;    // query blocks, key splits, key tiles (of 64) per split
-  float* opart;                // nsplit > 1: unnormalised partial O [nsplit][b*h][lq][padded d]
+  float* opart;                // nsplit > 1: partial O [nsplit][b*h][lq][padded d]: f16 O / sum, or f32 O (bf16)
   float* ml;                   // nsplit > 1: running (max, sum) [nsplit][b*h][lq][2]
   const float* rcos;           // RoPE tables [rrows][d] (f32) for the first nrq queries, or null
   const float* rsin;

@@ -319,19 +319,35 @@ __global__ __launch_bounds__(f256::kThreads) void flash256_kernel(FlashParams p)
         *reinterpret_cast<typename Vec<T>::x4*>(orow + d0) = w4;
       }
   } else {
-    // unnormalised partial O [split][bh][q][256] (f32) and (max, sum) [split][bh][q][2]
+    // partial O [split][bh][q][256] and (max, sum) [split][bh][q][2]: f16 stores O / sum (a convex
+    // combination of f16 values of v, so it stays in range), bf16 the unnormalised O in f32
     const long row = ((long)split * p.b * p.h + bhi) * p.lq + qidx;
-    float* prow = p.opart + row * 256;
+    if constexpr (__is_same(T, f16)) {
+      const float inv = 1.f / l;
+      f16* prow = reinterpret_cast<f16*>(p.opart) + row * 256;
 #pragma unroll
-    for (int ob = 0; ob < 8; ++ob)
+      for (int ob = 0; ob < 8; ++ob)
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int d0 = 32 * ob + 8 * a + 4 * hh;
-        f32x4 w4;
+        for (int a = 0; a < 4; ++a) {
+          const int d0 = 32 * ob + 8 * a + 4 * hh;
+          Vec<f16>::x4 w4;
 #pragma unroll
-        for (int bb = 0; bb < 4; ++bb) w4[bb] = o[ob][4 * a + bb];
-        *reinterpret_cast<f32x4*>(prow + d0) = w4;
-      }
+          for (int bb = 0; bb < 4; ++bb) w4[bb] = (f16)(o[ob][4 * a + bb] * inv);
+          *reinterpret_cast<Vec<f16>::x4*>(prow + d0) = w4;
+        }
+    } else {
+      float* prow = p.opart + row * 256;
+#pragma unroll
+      for (int ob = 0; ob < 8; ++ob)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const int d0 = 32 * ob + 8 * a + 4 * hh;
+          f32x4 w4;
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb) w4[bb] = o[ob][4 * a + bb];
+          *reinterpret_cast<f32x4*>(prow + d0) = w4;
+        }
+    }
     if (hh == 0) {
       float2 ml;
       ml.x = m_run;
