@@ -301,10 +301,13 @@ template <typename T, int VEC, int NC>
 static hipError_t launch_gather(const void* value, PointSrc<T> src, void* out, int b, int s, int q, int h, int d, int l,
                                 int p, const Levels& lv, hipStream_t stream) {
   const int lanes = d / VEC;
-  int shift = 3;
+  const int ntab = (l * p * 4 + kDeformUnroll - 1) / kDeformUnroll * kDeformUnroll;
+  // as few lanes per pair as cover a corner row (4 for 16-bit D = 32: every lane of a gather busy),
+  // but at least 8 when the corner tables of 16 pairs per wave would pass 64 KB of LDS
+  int shift = 2;
+  if ((size_t)(kDeformThreads / 64) * 16 * ntab * sizeof(int2) > 65536) shift = 3;
   while ((1 << shift) < lanes && shift < 6) ++shift;
   const int ppw = 64 >> shift;
-  const int ntab = (l * p * 4 + kDeformUnroll - 1) / kDeformUnroll * kDeformUnroll;
   const long pairs = (long)b * q * h;
   const long waves = (pairs + ppw - 1) / ppw;
   const long blocks = (waves + kDeformThreads / 64 - 1) / (kDeformThreads / 64);
