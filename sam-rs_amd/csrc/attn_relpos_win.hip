@@ -20,8 +20,10 @@
 //     slots at hd 64 in one);
 //   * all data moves by LDS DMA (global_load_lds): the q rows, the table and tile 0 are requested at
 //     once, q into ring buffer 1 and the table into buffer 2, which tiles 1 and 2 take over once the
-//     bias prologue has read them; tile 3 then goes into buffer 0. The two halves of a unit are
-//     adjacent workgroups on one XCD, so the second half's K and V come from L2;
+//     bias prologue has read them; tile 3 then goes into buffer 0. Both halves of a unit run on one
+//     XCD. In a grid of more than two rounds they are adjacent workgroups, so the second half's K and
+//     V come from L2. In a smaller grid all first halves go first, so that the last round holds the
+//     lighter second halves;
 //   * each wave waits only for its own DMAs of what it needs next (s_waitcnt vmcnt: a wave's vector
 //     memory operations complete in issue order), then one barrier publishes everyone's share;
 //   * kT tiles are stored [d][64 slots] with the 8-byte chunks of each row XOR-swizzled by the row's
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
                                                                        const T* __restrict__ v,
                                                                        const T* __restrict__ table,
                                                                        T* __restrict__ out, int H, int W,
-                                                                       float scale) {
+                                                                       float scale, int nunits, int n8) {
   using namespace win;
   typedef Shape<HD> S;
   constexpr int kKS = S::kKS, kMBO = S::kMBO, kTile = S::kTile, kBuf = S::kBuf, kTDma = S::kTDma;
@@ -123,9 +125,21 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   const int n = lane & 31, hh = lane >> 5;
   const int g = lane >> 4, gi = lane & 15;
   const long unit_elems = (long)N * HD;
-  const int blk = win_xcd_block(blockIdx.x, gridDim.x);
-  const long u = blk >> 1;
-  const int q0 = (blk & 1) * kQRows;  // first query of this half unit
+  // Work order. n8 > 0: all first halves (workgroups [0, n8)), then all second halves; n8 is the unit
+  // count rounded up to a multiple of 8, so both halves of a unit run on the same XCD (workgroup i
+  // runs on XCD i % 8). n8 == 0: the halves of a unit are adjacent, in contiguous ranges per XCD.
+  long u;
+  int half;
+  if (n8 > 0) {
+    half = blockIdx.x >= (unsigned)n8;
+    u = (long)blockIdx.x - half * n8;
+  } else {
+    const int blk = win_xcd_block(blockIdx.x, gridDim.x);
+    u = blk >> 1;
+    half = blk & 1;
+  }
+  if (u >= nunits) return;  // padding workgroup (n8 > 0): nothing issued, no barrier reached
+  const int q0 = half * kQRows;  // first query of this half unit
   const int qidx = q0 + wave * 32 + n;
   const bool qvalid = qidx < N;
   // qidx < 256 and W <= 16: (qidx + 0.5) / W lies at least 0.5 / W from an integer, far beyond the
@@ -421,8 +435,14 @@ static hipError_t launch_win(const void* q, const void* kt, const void* v, const
   constexpr size_t lds = win::Shape<HD>::kLdsBytes;
   static std::atomic<unsigned long long> lds_done{0};
   if (const hipError_t e = lds_opt_in(lds_done, (const void*)kern, (int)lds); e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3((unsigned)(2 * bh)), dim3(win::kThreads), lds, stream, (const T*)q,
-                     (const T*)kt, (const T*)v, (const T*)table, (T*)out, h, w, scale);
+  // When the grid fits in two rounds of the chip's workgroup slots, the second round should hold the
+  // lighter second halves (68 of 196 queries at 14x14), so all first halves go first. Larger grids
+  // keep the halves of a unit adjacent, so that the second half reads K and V from L2.
+  const long slots = (long)device_cu_count() * (HD == 64 ? 3 : 2);
+  const int n8 = bh <= slots ? (bh + 7) / 8 * 8 : 0;
+  const unsigned grid = n8 > 0 ? (unsigned)(2 * n8) : (unsigned)(2 * bh);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(win::kThreads), lds, stream, (const T*)q, (const T*)kt, (const T*)v,
+                     (const T*)table, (T*)out, h, w, scale, bh, n8);
   return hipGetLastError();
 }
 

@@ -23,6 +23,22 @@ inline hipError_t lds_opt_in(std::atomic<unsigned long long>& done, const void* 
   return e;
 }
 
+// Compute units of the current device, read once per device (at most 64 devices cached; 256 if the
+// query fails).
+inline int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return 256;
+  if (dev >= 0 && dev < 64) cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
 typedef _Float16 f16;
 typedef __bf16 bf16;
 
