@@ -21,8 +21,9 @@
 // Few query blocks (SAM 2 memory attention: one head, 4096 queries, 4096 or 28736 keys) would leave
 // most of the 256 CUs idle, so the keys are split across workgroups; each split writes a partial O
 // (f16: normalised by its own sum, in f16, half the bytes of f32; bf16: unnormalised, in f32) with its
-// running max and sum, and flash_combine_kernel merges the splits by log-sum-exp. Workgroups are numbered XCD-major with all query blocks of one (head, split) adjacent,
-// so the K/V range of a split is fetched into one XCD's L2 and shared there.
+// running max and sum, and flash_combine_kernel merges the splits by log-sum-exp. Workgroups are
+// numbered XCD-major with all query blocks of one (head, split) adjacent, so the K/V range of a split
+// is fetched into one XCD's L2 and shared there.
 //
 // Optional RoPE on the queries (the first n_rope_q rows, table row = query % rope_rows) is applied while
 // Q is loaded, in f32 with the reference's rounding (x*cos + rot(x)*sin, rot([x0,x1]) = [-x1,x0],
@@ -360,33 +361,68 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
 }
 
 // out[b, q, h, :] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, M = max_s m_s, with O_s the
-// unnormalised partial (bf16: f32 partials) or l_s times the stored O_s / l_s (f16: f16 partials). One
-// wave per row, each lane 4 consecutive columns.
+// unnormalised partial (bf16: f32 partials) or l_s times the stored O_s / l_s (f16: f16 partials).
+// A row takes DP / 8 lanes of 8 consecutive columns each (one 16-byte read per split of an f16
+// partial, two of an f32 one), so a workgroup merges 256 / (DP / 8) rows.
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p) {
-  const int lane = threadIdx.x & 63;
-  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);  // (bh, q)
+  constexpr int LPR = DP / 8;     // lanes per row
+  constexpr int RPB = 256 / LPR;  // rows per workgroup (DP 96: 21, and 4 idle threads)
+  if (threadIdx.x >= RPB * LPR) return;
+  const int c = 8 * (threadIdx.x % LPR);
+  const long row = (long)blockIdx.x * RPB + threadIdx.x / LPR;  // (bh, q)
   const long rows = (long)p.b * p.h * p.lq;
   if (row >= rows) return;
   const long plane = rows;
-  float mx = -INFINITY;
-  for (int s = 0; s < p.nsplit; ++s) mx = fmaxf(mx, p.ml[(s * plane + row) * 2]);
-  float den = 0.f;
-  f32x4 acc = f32x4{};
-  const int c = 4 * lane;
-  for (int s = 0; s < p.nsplit; ++s) {
-    const float w = exp2_fast(p.ml[(s * plane + row) * 2] - mx);
-    const float wl = w * p.ml[(s * plane + row) * 2 + 1];
-    den += wl;
-    if (c < DP) {
-      if constexpr (__is_same(T, f16)) {
-        const Vec<f16>::x4 o4 = *reinterpret_cast<const Vec<f16>::x4*>(reinterpret_cast<const f16*>(p.opart) +
-                                                                      (s * plane + row) * DP + c);
+  // splits in chunks of 8: every (max, sum) and partial read of a chunk is issued before any is used;
+  // a later chunk with a larger max rescales what is summed so far (one chunk up to 8 splits)
+  float mx = -INFINITY, den = 0.f;
+  float acc[8] = {};
+  for (int s0 = 0; s0 < p.nsplit; s0 += 8) {
+    float2 ml[8];
+    float o[8][8];
 #pragma unroll
-        for (int bb = 0; bb < 4; ++bb) acc[bb] += wl * (float)o4[bb];
+    for (int j = 0; j < 8; ++j) {
+      const long r = ((long)(s0 + j) * plane + row);
+      if (s0 + j < p.nsplit) {
+        ml[j] = *reinterpret_cast<const float2*>(p.ml + r * 2);
+        if constexpr (__is_same(T, f16)) {
+          const f16x8 o8 = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(p.opart) + r * DP + c);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) o[j][k] = (float)o8[k];
+        } else {
+          const f32x4* src = reinterpret_cast<const f32x4*>(p.opart + r * DP + c);
+          const f32x4 a = src[0], b = src[1];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            o[j][k] = a[k];
+            o[j][4 + k] = b[k];
+          }
+        }
       } else {
-        acc += w * *reinterpret_cast<const f32x4*>(p.opart + (s * plane + row) * DP + c);
+        ml[j] = make_float2(-INFINITY, 0.f);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[j][k] = 0.f;
       }
+    }
+    float cm = mx;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cm = fmaxf(cm, ml[j].x);
+    if (s0 > 0) {
+      const float r = exp2_fast(mx - cm);
+      den *= r;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k] *= r;
+    }
+    mx = cm;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float w = exp2_fast(ml[j].x - mx);
+      const float wl = w * ml[j].y;
+      den += wl;
+      const float f = __is_same(T, f16) ? wl : w;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k] += f * o[j][k];
     }
   }
   if (c >= p.d) return;
@@ -394,10 +430,10 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p) {
   const int bhi = (int)(row / p.lq), q = (int)(row % p.lq);
   const int bi = bhi / p.h, head = bhi % p.h;
   T* orow = reinterpret_cast<T*>(p.out) + bi * p.so[0] + head * p.so[2] + (long)q * p.so[1];
-  typename Vec<T>::x4 w4;
+  typename Vec<T>::x8 w8;
 #pragma unroll
-  for (int bb = 0; bb < 4; ++bb) w4[bb] = from_f32<T>(acc[bb] * inv);
-  *reinterpret_cast<typename Vec<T>::x4*>(orow + c) = w4;
+  for (int j = 0; j < 8; ++j) w8[j] = from_f32<T>(acc[j] * inv);
+  *reinterpret_cast<typename Vec<T>::x8*>(orow + c) = w8;
 }
 
 // ---------------------------------------------------------------------------------------------- launch
@@ -419,7 +455,9 @@ static hipError_t launch_flash(FlashParams p, bool ropeq, hipStream_t stream) {
   }
   if (e != hipSuccess || p.nsplit == 1) return e;
   const long rows = (long)p.b * p.h * p.lq;
-  hipLaunchKernelGGL((flash_combine_kernel<T, DP>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, p);
+  constexpr int kRowsPerBlock = 256 / (DP / 8);
+  hipLaunchKernelGGL((flash_combine_kernel<T, DP>), dim3((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
+                     dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
