@@ -281,12 +281,15 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
 
         ms = timer.avg_ms(run, 50)
         nbytes = 4.0 * (s * hh * dd + 3 * q * hh * ll * pp + q * hh * dd)
+        gathered = 4.0 * q * hh * ll * pp * 4 * dd
         res[f"dino_deform_{name}_f32"] = {
             "workload": f"Grounding DINO-tiny deformable attention, {q} queries over {s} values, 8 heads x 32, "
                         "4 levels x 4 points",
             "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            # the corner rows the gather delivers to registers (4 per point, D f32 each)
+            "gathered_bytes": gathered, "gathered_gbs": round(gathered / (ms * 1e-3) / 1e9, 1),
         }
         if cpu:
             vh, lh, ah = host(value), host(loc), host(attn_w)
@@ -313,6 +316,7 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
             "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "gathered_bytes": gathered, "gathered_gbs": round(gathered / (ms * 1e-3) / 1e9, 1),
         }
         if cpu:
             oh, gh, rh = host(off), host(logits), host(refs)
