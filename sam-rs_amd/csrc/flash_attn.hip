@@ -28,7 +28,7 @@
 // Optional RoPE on the queries (the first n_rope_q rows, table row = query % rope_rows) is applied while
 // Q is loaded, in f32 with the reference's rounding (x*cos + rot(x)*sin, rot([x0,x1]) = [-x1,x0],
 // sam3/video.rs:106-113) and then rounded to the element type as the reference's rope does. Keys are
-// rotated beforehand by rope_rows_kernel (rope.hip).
+// rotated beforehand by rope_shared_kernel (rope.hip).
 #include "flash_attn.hpp"
 
 namespace samhip {

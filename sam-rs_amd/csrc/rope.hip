@@ -7,52 +7,91 @@
 // the reference's rope (sam3/video.rs:106-113: f32 arithmetic, each product and the sum rounded, then
 // converted back to the element type) together with RopeAttn's key handling (sam3/video.rs:133-141:
 // the tables tiled over the first M - n_exclude keys, the object-pointer keys left as they are).
-// One thread per 8 contiguous elements; bound by HBM (x read once, out written once, the f32 tables
-// read from L2). For f16 / bf16 one launch can rotate two row sets (an attention call's keys and queries).
+// f16 / bf16: rope_shared_kernel, which reads each piece of the tables once for every row that uses it;
+// one launch can rotate two row sets (an attention call's keys and queries). f32: one thread per 4
+// contiguous elements. Bound by HBM (x read once, out written once).
+#include <algorithm>
+
 #include "flash_attn.hpp"
 
 namespace samhip {
 
+// Rotation with shared table reads: a thread owns (batch*head, table row t, 8 columns), reads that
+// piece of the cos and sin tables once, and rotates every row r = t (mod trows), r < nrot, of both row
+// sets (the cross-attention keys use each table row 7 times, and the queries once more). The threads
+// past the rotation part copy the rows r >= nrot. Same arithmetic per element as rope_rows_one.
 template <typename T>
-__device__ __forceinline__ void rope_rows_one(const RopeJob& jb, int d, const float* __restrict__ cos_t,
-                                              const float* __restrict__ sin_t, int trows, long c) {
+__device__ __forceinline__ void rope_rotate_rows(const RopeJob& jb, long bhx, int t, int c8, int trows,
+                                                 const float* cs, const float* sn) {
   typedef typename Vec<T>::x8 X8;
-  if (c >= jb.total) return;
-  const int cpr = d / 8;
-  const int c8 = (int)(c % cpr) * 8;
-  const long rowi = c / cpr;  // (b, r, h)
-  const int hi = (int)(rowi % jb.h);
-  const long br = rowi / jb.h;
-  const int r = (int)(br % jb.l);
-  const long bi = br / jb.l;
-  const T* x = reinterpret_cast<const T*>(jb.x);
-  T* out = reinterpret_cast<T*>(jb.out);
-  const X8 xv = *reinterpret_cast<const X8*>(x + bi * jb.sx[0] + r * jb.sx[1] + hi * jb.sx[2] + c8);
-  X8 yv = xv;
-  if (r < jb.nrot) {
-#pragma clang fp contract(off)  // the reference rounds each product and the sum: no FMA
-    const long tr = (long)(r % trows) * d + c8;
-    float y[8];
+  if (bhx >= (long)jb.b * jb.h || t >= jb.nrot) return;
+  const int hi = (int)(bhx % jb.h);
+  const long bi = bhx / jb.h;
+  const T* x = reinterpret_cast<const T*>(jb.x) + bi * jb.sx[0] + hi * jb.sx[2] + c8;
+  T* out = reinterpret_cast<T*>(jb.out) + bi * jb.so[0] + hi * jb.so[2] + c8;
+  for (int r0 = t; r0 < jb.nrot; r0 += 4 * trows) {
+    X8 xv[4];
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-      const float x0 = to_f32(xv[j]), x1 = to_f32(xv[j + 1]);
-      y[j] = x0 * cos_t[tr + j] + -x1 * sin_t[tr + j];
-      y[j + 1] = x1 * cos_t[tr + j + 1] + x0 * sin_t[tr + j + 1];
+    for (int u = 0; u < 4; ++u) {
+      const int r = r0 + u * trows;
+      if (r < jb.nrot) xv[u] = *reinterpret_cast<const X8*>(x + (long)r * jb.sx[1]);
     }
-    yv = pack8(y, (X8*)nullptr);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int r = r0 + u * trows;
+      if (r < jb.nrot) {
+#pragma clang fp contract(off)  // the reference rounds each product and the sum: no FMA
+        float y[8];
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          const float x0 = to_f32(xv[u][j]), x1 = to_f32(xv[u][j + 1]);
+          y[j] = x0 * cs[j] + -x1 * sn[j];
+          y[j + 1] = x1 * cs[j + 1] + x0 * sn[j + 1];
+        }
+        *reinterpret_cast<X8*>(out + (long)r * jb.so[1]) = pack8(y, (X8*)nullptr);
+      }
+    }
   }
-  *reinterpret_cast<X8*>(out + bi * jb.so[0] + r * jb.so[1] + hi * jb.so[2] + c8) = yv;
 }
 
-// Up to two row sets in one launch (the keys and the queries of one attention call): blocks below
-// blocks_a work on job a, the rest on job b.
 template <typename T>
-__global__ __launch_bounds__(256) void rope_rows_kernel(RopeJob a, RopeJob b, long blocks_a, int d,
-                                                        const float* __restrict__ cos_t,
-                                                        const float* __restrict__ sin_t, int trows) {
-  const long blk = blockIdx.x;
-  if (blk < blocks_a) rope_rows_one<T>(a, d, cos_t, sin_t, trows, blk * 256 + threadIdx.x);
-  else rope_rows_one<T>(b, d, cos_t, sin_t, trows, (blk - blocks_a) * 256 + threadIdx.x);
+__global__ __launch_bounds__(256) void rope_shared_kernel(RopeJob a, RopeJob b, int d, const float* __restrict__ cos_t,
+                                                          const float* __restrict__ sin_t, int trows, int tused,
+                                                          long nrt, long ncopy_a, long ncopy_b) {
+  typedef typename Vec<T>::x8 X8;
+  const long c = (long)blockIdx.x * 256 + threadIdx.x;
+  const int cpr = d / 8;
+  if (c < nrt) {
+    const int c8 = (int)(c % cpr) * 8;
+    const long rest = c / cpr;
+    const int t = (int)(rest % tused);
+    const long bhx = rest / tused;
+    const long tr = (long)t * d + c8;
+    float cs[8], sn[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      cs[j] = cos_t[tr + j];
+      sn[j] = sin_t[tr + j];
+    }
+    rope_rotate_rows<T>(a, bhx, t, c8, trows, cs, sn);
+    rope_rotate_rows<T>(b, bhx, t, c8, trows, cs, sn);
+    return;
+  }
+  long k = c - nrt;
+  if (k >= ncopy_a + ncopy_b) return;
+  const bool in_a = k < ncopy_a;
+  const RopeJob& jb = in_a ? a : b;
+  if (!in_a) k -= ncopy_a;
+  const int c8 = (int)(k % cpr) * 8;
+  const long rest = k / cpr;
+  const int nl = jb.l - jb.nrot;
+  const int r = jb.nrot + (int)(rest % nl);
+  const long bhx = rest / nl;
+  const int hi = (int)(bhx % jb.h);
+  const long bi = bhx / jb.h;
+  *reinterpret_cast<X8*>(reinterpret_cast<T*>(jb.out) + bi * jb.so[0] + (long)r * jb.so[1] + hi * jb.so[2] + c8) =
+      *reinterpret_cast<const X8*>(reinterpret_cast<const T*>(jb.x) + bi * jb.sx[0] + (long)r * jb.sx[1] +
+                                   hi * jb.sx[2] + c8);
 }
 
 // f32 rows: one thread per 4 contiguous elements.
@@ -105,12 +144,22 @@ hipError_t rope_rows2(int dtype, const RopeJob& a, const RopeJob* b, int d, cons
                       int trows, hipStream_t stream) {
   RopeJob none{};
   const RopeJob& jb = b ? *b : none;
-  const long ba = (a.total + 255) / 256, bb = (jb.total + 255) / 256;
-  const unsigned blocks = (unsigned)(ba + bb);
+  // the shared-table kernel: one thread per (batch*head, used table row, 8 columns), then one per 8
+  // columns of every row past nrot
+  const int cpr = d / 8;
+  const long bh = std::max((long)a.b * a.h, (long)jb.b * jb.h);
+  const int tused = std::min(trows, std::max(a.nrot, jb.nrot));
+  const long nrt = bh * tused * cpr;
+  const long ncopy_a = (long)a.b * a.h * (a.l - a.nrot) * cpr, ncopy_b = (long)jb.b * jb.h * (jb.l - jb.nrot) * cpr;
+  const long threads = nrt + ncopy_a + ncopy_b;
+  if (threads == 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((threads + 255) / 256);
   if (dtype == kF16)
-    hipLaunchKernelGGL(rope_rows_kernel<f16>, dim3(blocks), dim3(256), 0, stream, a, jb, ba, d, cos_t, sin_t, trows);
+    hipLaunchKernelGGL(rope_shared_kernel<f16>, dim3(blocks), dim3(256), 0, stream, a, jb, d, cos_t, sin_t, trows,
+                       tused, nrt, ncopy_a, ncopy_b);
   else
-    hipLaunchKernelGGL(rope_rows_kernel<bf16>, dim3(blocks), dim3(256), 0, stream, a, jb, ba, d, cos_t, sin_t, trows);
+    hipLaunchKernelGGL(rope_shared_kernel<bf16>, dim3(blocks), dim3(256), 0, stream, a, jb, d, cos_t, sin_t, trows,
+                       tused, nrt, ncopy_a, ncopy_b);
   return hipGetLastError();
 }
 
