@@ -8,7 +8,8 @@
 //
 // The work is streaming: each row is read once and written once (2 * N elements), so the kernel is
 // built around HBM traffic rather than arithmetic.
-//   * A wave owns 32 consecutive rows. Their bias dot products are one small GEMM, G = Table . Q^T
+//   * A wave owns 32 consecutive rows (16 for 16-bit rows of one vector per lane: the waves then cover
+//     twice as many rows in flight). Their bias dot products are one small GEMM, G = Table . Q^T
 //     (all (2H-1) + (2W-1) table rows against the 32 q rows), on the MFMA (32x32x16 f16/bf16,
 //     32x32x2 f32), one 32-row block of the table at a time. Each lane then holds one q row's
 //     products with 16 table rows and scatters those that fall on the row's diagonal band into a
@@ -33,7 +34,12 @@ namespace samhip {
 namespace rsm {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWaves = 4;   // waves per workgroup (independent)
-constexpr int kRows = 32;   // rows per wave
+constexpr int kRows = 32;   // rows per wave (bias scratch and the MFMA bias prologue: one 32-row block)
+// Rows a wave of the vector kernel runs. 16-bit rows of one vector per lane (ITEMS == 1, the 14x14
+// windows) are short, so a wave spends its time waiting on each group's loads and reductions; 16 rows
+// per wave double the waves in flight (the prologue's other 16 bias rows are computed and not used). In
+// f32 the prologue runs on the 32x32x2 MFMA and costs more than the waves gain, so f32 keeps 32.
+constexpr int vec_rows_per_wave(int items, int elem_bytes) { return items == 1 && elem_bytes == 2 ? 16 : kRows; }
 }  // namespace rsm
 
 // Wave64 reductions on the VALU, with no LDS round trip: DPP row rotations by 1, 2, 4 and 8 reduce each
@@ -227,11 +233,12 @@ __global__ __launch_bounds__(rsm::kWaves * 64) void relpos_softmax_vec_kernel(co
   static_assert(!AW || VE % 4 == 0, "vector Rw reads cover whole 16-byte runs");
   extern __shared__ float bias_lds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const long r0 = ((long)blockIdx.x * kWaves + wave) * kRows;
+  constexpr int RPW = vec_rows_per_wave(ITEMS, (int)sizeof(T));
+  const long r0 = ((long)blockIdx.x * kWaves + wave) * RPW;
   if (r0 >= rows) return;  // the waves of a workgroup share nothing
   float* bias = bias_lds + wave * kRows * bst;
   const int N = H * W, nvec = N / VE;
-  const int nrows = (int)min((long)kRows, rows - r0);
+  const int nrows = (int)min((long)RPW, rows - r0);
   // (kh << 16 | kw) of the first element of each of this lane's vectors: the same for every row
   int khw[ITEMS];
 #pragma unroll
@@ -398,7 +405,10 @@ static hipError_t launch_vec(const void* s, const void* q, const void* tab, void
   auto kern = relpos_softmax_vec_kernel<T, VB, ITEMS, AW>;
   static std::atomic<unsigned long long> done{0};
   if (const hipError_t e = lds_opt_in(done, (const void*)kern, (int)lds); e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(blocks), dim3(rsm::kWaves * 64), lds, stream, (const T*)s, (const T*)q,
+  (void)blocks;  // the 32-row count of the scalar kernel; this kernel's waves run vec_rows_per_wave rows
+  const long rows_per_block = (long)rsm::kWaves * rsm::vec_rows_per_wave(ITEMS, (int)sizeof(T));
+  const unsigned nblocks = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
+  hipLaunchKernelGGL(kern, dim3(nblocks), dim3(rsm::kWaves * 64), lds, stream, (const T*)s, (const T*)q,
                      (const T*)tab, (T*)out, rows, h, w, hd, scale, bst);
   return hipGetLastError();
 }
