@@ -126,6 +126,33 @@ def test_rope_leaves_excluded_rows(hip):
     assert np.array_equal(got[:32], want)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("side,l,n_rot", [(2, 37, 30), (4, 37, 30), (4, 70, 70)])
+def test_rope_batches_heads_and_tiled_tables(hip, side, l, n_rot, dtype):
+    """Several batches and heads, a [B, H, L, D] view (strided rows), tables of side*side rows reused by
+    up to 8 rows each (row r takes table row r % T), and rows past n_rot copied: bit-exact against the
+    oracle's rope row by row."""
+    b, h, d = 2, 3, 64
+    cos, sin = oracle.rope_tables(side, 1.0, d, 10000.0)
+    trows = side * side
+    r = np.random.default_rng(7 + l + side)
+    x = rounded(r, (b, h, l, d), dtype)
+    xd = to_dev(x, dtype).permute(0, 2, 1, 3)  # [B, L, H, D] view of the [B, H, L, D] tensor
+    print(f"rope b={b} h={h} l={l} trows={trows} n_rot={n_rot} {dtype}", flush=True)
+    got = hip.rope(xd, torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda(), n_rot=n_rot)
+    torch.cuda.synchronize()
+    got = got.float().cpu().numpy()  # [B, L, H, D]
+    for bi in range(b):
+        for hi in range(h):
+            rows = x[bi, hi]
+            want = rows.copy()
+            for rr in range(n_rot):
+                t = rr % trows
+                want[rr] = oracle.rope(rows[rr:rr + 1], cos[t:t + 1], sin[t:t + 1])[0]
+            want = oracle.round_to(want, dtype)
+            assert np.array_equal(got[bi, :, hi], want), (bi, hi)
+
+
 def memory_inputs(side, frames, n_ptr, d, dtype, seed):
     r = np.random.default_rng(seed)
     n = side * side
