@@ -87,6 +87,15 @@ __device__ __forceinline__ f32x16 mma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// D(16x16, f32) += A(16x32) * B(32x16). Lane l supplies A[l%16][8*(l/16)+j] and B[8*(l/16)+j][l%16],
+// j = 0..7; it receives D[4*(l/16) + i][l%16] in element i.
+__device__ __forceinline__ f32x4 mma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 // LDS transpose read (ds_read_b64_tr_b16). Within each group of 16 lanes, lane i receives element
 // (i % 4) of the 4 x 16-bit values addressed by lanes 4*s + i/4 of its group, in element s (s = 0..3).
 // So if lane 4*s + c of the group points at row (k0 + s) of a row-major tile, at column n0 + 4*c,
@@ -113,6 +122,18 @@ __device__ __forceinline__ float max_with_partner32(float x) {
 __device__ __forceinline__ float sum_with_partner32(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Max and sum over the four lanes l % 16 + 16 g (g = 0..3) of a 16-lane column: v_permlane16_swap
+// exchanges the odd 16-lane rows of its first operand with the even rows of its second, so with both
+// operands = x the pair holds x[l] and x[l ^ 16]; permlane32_swap then pairs l and l ^ 32.
+__device__ __forceinline__ float max_over_rows16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return max_with_partner32(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+__device__ __forceinline__ float sum_over_rows16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return sum_with_partner32(__uint_as_float(r[0]) + __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -20,14 +20,28 @@ struct FlashParams {
   const float* rcos;           // RoPE tables [rrows][d] (f32) for the first nrq queries, or null
   const float* rsin;
   int rrows, nrq;
+  void* vt;                    // head dim 256: V as transposed key tiles (flash_vt.hpp), flash256_vt_bytes
+  int vt_ready;                // the tiles are already written (by the rotation launch)
 };
+
+// V of a head-dim-256 call, to be written as transposed key tiles at vt (flash_vt.hpp).
+struct VtJob {
+  const void* v;
+  long sv[3];
+  int b, h, lk;
+  void* vt;
+};
+long flash256_vt_blocks(const VtJob& j);                                // workgroups of its pass (256 threads)
+hipError_t flash256_vt(const VtJob& j, hipStream_t stream);             // the pass as a launch of its own
 
 int flash_padded_dim(int d);
 int flash_queries_per_block(int d);
 void flash_plan(int b, int h, int lq, int lk, int d, int cus, int* qblocks, int* nsplit, int* tps);
 size_t flash_partial_bytes(int b, int h, int lq, int d, int nsplit);
 hipError_t flash_attn_half(int dtype, FlashParams p, bool ropeq, hipStream_t stream);
-// The head-dim-256 kernel (flash_attn_d256.hip): whether it takes p, and its launch (main kernel only).
+// The head-dim-256 kernel (flash_attn_d256.hip): the bytes of its transposed V tiles, whether it takes
+// p, and its launch (the V tile pass and the main kernel; not the combine).
+size_t flash256_vt_bytes(int b, int h, int lk, int d);
 bool flash256_eligible(const FlashParams& p, int elem_bytes);
 hipError_t flash256_launch(int dtype, FlashParams p, bool ropeq, hipStream_t stream);
 
@@ -44,8 +58,9 @@ struct RopeJob {
   long total;
 };
 RopeJob rope_job(const void* x, const long* sx, void* out, const long* so, int b, int l, int h, int d, int nrot);
-// rope_rows over job a and, if b is not null, job b in one launch (f16 / bf16; both with head dim d).
+// rope_rows over job a and, if b is not null, job b in one launch (f16 / bf16; both with head dim d);
+// if vt is not null, the same launch also writes that V as transposed key tiles.
 hipError_t rope_rows2(int dtype, const RopeJob& a, const RopeJob* b, int d, const float* cos_t, const float* sin_t,
-                      int trows, hipStream_t stream);
+                      int trows, hipStream_t stream, const VtJob* vt = nullptr);
 
 }  // namespace samhip

@@ -3,42 +3,48 @@
 // Same contract and numerics as flash_fwd_kernel (flash_attn.hip): out = softmax(scale q k^T) v per
 // (batch, head), the reference's mask-free sdpa / flash_attn (sam3/nn.rs:26-34, sam3/video.rs:129-145),
 // exp2-domain online softmax with a lazy rescale, optional RoPE on q, and key splits merged by
-// flash_combine_kernel. What differs is the register and staging plan, chosen for d = 256 where the O^T
-// accumulators alone take 128 registers per lane:
+// flash_combine_kernel. What differs is the register and LDS plan, chosen for d = 256, where a wave of
+// 32 queries needs 128 registers per lane for O^T alone and so runs alone on its SIMD:
 //
-// - One wave per SIMD (4 waves x 32 queries). O^T (128) and the scores S^T (32) live in accumulation
-//   registers; Q (64), addresses and the softmax work in arithmetic registers. No C++ arithmetic touches
-//   O^T inside the key loop (the rare rescale is done by accumulation-register reads and writes), so the
-//   compiler keeps O^T where the MFMAs accumulate it instead of shadowing it in arithmetic registers.
-// - K and V tiles (64 keys x 512 bytes) go from global memory straight into LDS by buffer-descriptor
-//   DMA (buffer_load_dwordx4 ... lds), so no staging registers are live. The descriptor of a tile ends
-//   after the last valid key row, so rows past the end read as zero.
-// - The 512-byte rows are stored unpadded (a DMA writes 1 KB contiguously) with the 16-byte chunks of a
-//   row permuted by an XOR of the row index: chunk ^ (row & 15) for K (its rows are read 16 bytes per
-//   lane, 32 rows at once) and chunk ^ 4 (row & 7) for V (its transpose reads touch 8 rows x 64 bytes).
-//   Both read patterns then spread over all banks.
-// - Buffers: V0, V1, K0, K1, 32 KB each, so every LDS read is one of 16 per-lane base registers plus an
-//   instruction offset.
+// - Two waves per SIMD (8 waves x 16 queries, 128 queries per workgroup, the query block of the other
+//   kernels). A wave holds S^T (16 registers), O^T (64) and its Q fragments (32) for
+//   v_mfma_f32_16x16x32; with about half the register file per wave, one wave's LDS and MFMA latency
+//   is covered by the other's work.
+// - Every LDS read is a 16-byte ds_read_b128 whose row is the MFMA's reduction dimension. K rows
+//   (key-major, d contiguous) already are. V is not: a pass before the kernel writes each 64-key tile
+//   of V as V^T, 256 rows of 64 keys, in the exact byte image the kernel wants in LDS (flash_vt.hpp),
+//   so the tile moves by plain 1 KB DMAs. The pass rides in the launch that rotates the keys when
+//   there is one, else it is a launch of its own. Against transpose reads (ds_read_b64_tr_b16, 8
+//   bytes per lane) this halves the LDS read instructions of P.V, which with 16 queries per wave
+//   would otherwise bound the kernel.
+// - K and V^T tiles (32 KB each) go from global memory straight into LDS by DMA (buffer_load_dwordx4
+//   ... lds / global_load_lds_dwordx4), double-buffered: K0, K1, V0, V1 = 128 KB, one workgroup per
+//   CU. The K descriptor of a tile ends after the last valid key row, so rows past the end read as 0.
+// - Bank layout: K rows are 512 bytes; 16-byte chunk c of row r is stored at c ^ (r & 15), so the 16
+//   rows at one chunk that a quarter wave reads fall on 16 distinct 16-byte bank groups. V^T rows are
+//   128 bytes; chunk q of row r at q ^ ((r >> 1) & 7) does the same.
 // - One barrier per tile: step t issues the DMAs of tile t+1 into the buffers that step t-1 finished
 //   with, computes S^T = K Q^T, the softmax and O^T += V^T P^T of tile t, then waits for its DMAs.
 #include "flash_attn.hpp"
+#include "flash_vt.hpp"
 #include "lds_dma.hpp"
 
 namespace samhip {
 
 namespace f256 {
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kRow = 512;                     // bytes per key row (256 x 16-bit)
-constexpr int kTileBytes = 64 * kRow;         // 32 KB
-constexpr int kV0 = 0, kK0 = 2 * kTileBytes;  // V0, V1, K0, K1
+constexpr int kQ = 16;                        // queries per wave
+constexpr int kRow = 512;                     // bytes per K row (256 x 16-bit)
+constexpr int kVRow = 128;                    // bytes per V^T row (64 keys x 16-bit)
+constexpr int kTileBytes = 64 * kRow;         // 32 KB: a K tile, or a V^T tile (256 rows)
+constexpr int kK0 = 0, kV0 = 2 * kTileBytes;  // K0, K1, V0, V1
 constexpr int kLds = 4 * kTileBytes;          // 128 KB
 constexpr float kSlack = 8.0f;
-constexpr int kQkAhead = 5;  // k-steps of K fragments in flight ahead of the S^T MFMAs
-// Where in a step the four DMA groups of the next tile (K rows 0-7, K 8-15, V 0-7, V 8-15 of each
-// wave's share) are issued: 0 top of the step, 1 after S^T, 2 after the softmax, 3 halfway through P.V,
-// 4 inside S^T right after its first K reads.
-constexpr int kDmaAt[4] = {0, 0, 1, 1};
+constexpr int kAhead = 8;  // LDS fragments in flight ahead of their MFMAs
+static_assert(kWaves * kQ == 128, "the query block of flash_queries_per_block(256)");
+
+static_assert(kTileBytes == vtl::kTileBytes, "V^T tile size");
 }  // namespace f256
 
 // Workgroup i runs on XCD i % 8; give each XCD a contiguous range of the linear work index.
@@ -54,21 +60,8 @@ __device__ __forceinline__ void f256_rope_pair(float x0, float x1, float c0, flo
   y1 = x1 * c1 + x0 * s1;
 }
 
-// o[ob] *= alpha, element by element in accumulation registers. The leading s_nops cover the
-// MFMA-result-to-read latency (at most 19 wait states), the trailing one the write-to-MFMA-source latency.
-__device__ __forceinline__ void f256_rescale(f32x16* o, float alpha) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-#pragma unroll
-  for (int ob = 0; ob < 8; ++ob)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      float tmp;
-      asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
-                   : "+a"(o[ob][e]), "=&v"(tmp)
-                   : "v"(alpha));
-    }
-  asm volatile("s_nop 4" ::: "memory");
-}
+// The V^T tile pass as a launch of its own (calls whose keys are not rotated).
+__global__ __launch_bounds__(256) void flash256_vt_kernel(VtJob j) { flash256_vt_quarter(j, blockIdx.x); }
 
 template <typename T, bool ROPEQ>
 __global__ __launch_bounds__(f256::kThreads) void flash256_kernel(FlashParams p) {
@@ -81,8 +74,8 @@ __global__ __launch_bounds__(f256::kThreads) void flash256_kernel(FlashParams p)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = lane & 31, hh = lane >> 5;
-  const int g = lane >> 4, gi = lane & 15;
+  const int n = lane & 15, g = lane >> 4;     // MFMA column (query of the wave) and row group
+  const int n32 = lane & 31, hh = lane >> 5;  // DMA: 16-byte slot of a 512-byte row, and which row
 
   const int lin = f256_xcd_block(blockIdx.x, gridDim.x);
   const int qb = lin % p.qblocks;
@@ -90,53 +83,52 @@ __global__ __launch_bounds__(f256::kThreads) void flash256_kernel(FlashParams p)
   const int bhi = lin / (p.qblocks * p.nsplit);
   const int bi = bhi / p.h, head = bhi % p.h;
 
-  const int q0 = qb * (kWaves * 32) + wave * 32;
+  const int q0 = qb * (kWaves * kQ) + wave * kQ;
   const bool active = q0 < p.lq;
   const int qidx = q0 + n;
   const bool qvalid = qidx < p.lq;
 
+  const int ntiles = (p.lk + 63) >> 6;
   const int t_begin = split * p.tps;
-  const int t_end = min((p.lk + 63) >> 6, t_begin + p.tps);
+  const int t_end = min(ntiles, t_begin + p.tps);
   const int kend = p.lk;
 
   const T* qbase = reinterpret_cast<const T*>(p.q) + bi * p.sq[0] + head * p.sq[2];
   const T* kbase = reinterpret_cast<const T*>(p.k) + bi * p.sk[0] + head * p.sk[2];
-  const T* vbase = reinterpret_cast<const T*>(p.v) + bi * p.sv[0] + head * p.sv[2];
-  const long krow = p.sk[1] * (long)sizeof(T), vrow = p.sv[1] * (long)sizeof(T);  // row strides, bytes
+  const char* vtbase = reinterpret_cast<const char*>(p.vt) + (size_t)bhi * ntiles * kTileBytes;
+  const long krow = p.sk[1] * (long)sizeof(T);  // K row stride, bytes
 
-  // ---- DMA of one tile: 32 blocks of 1 KB (two key rows each); wave w moves rows 16w .. 16w+15.
-  // Block j of the wave holds rows 16w + 2j + hh; lane slot n of a row holds the row's chunk n ^ swz(row).
-  // The wave's LDS base is re-derived per call (opaque), so the 16 per-block LDS addresses are formed
-  // next to their DMAs instead of being held in scalar registers across the loop.
-  auto dma_tile = [&](const T* base, long rowb, int t, unsigned lds_tile, bool is_k, int j0, int j1) {
+  // K tile t into buffer buf: wave w moves rows 8w .. 8w+7 as 4 blocks of 1 KB (block j: rows
+  // 8w + 2j + hh); lane slot n32 of a row holds the row's chunk n32 ^ (row & 15)
+  auto dma_k = [&](int t, int buf) {
     const long r0 = (long)t * 64;
-    const unsigned bytes = (unsigned)min((kend - 1 - r0) * rowb + kRow, 0xffffffffL);  // through the last valid row
-    const i32x4 rs = buffer_rsrc(reinterpret_cast<const char*>(base) + r0 * rowb, bytes);
-    unsigned lb = lds_tile + 16 * wave * kRow;
+    const unsigned bytes = (unsigned)min((kend - 1 - r0) * krow + kRow, 0xffffffffL);  // through the last valid row
+    const i32x4 rs = buffer_rsrc(reinterpret_cast<const char*>(kbase) + r0 * krow, bytes);
+    unsigned lb = lds0 + kK0 + buf * kTileBytes + 8 * wave * kRow;
     asm volatile("" : "+s"(lb));
 #pragma unroll
-    for (int j = j0; j < j1; ++j) {
-      const int row = 16 * wave + 2 * j + hh;
-      const int swz = is_k ? ((2 * j + hh) & 15) : 4 * ((2 * j + hh) & 7);
-      const unsigned off = (unsigned)(row * rowb) + 16u * (unsigned)(n ^ swz);
-      bdma16(rs, off, lb + 2 * j * kRow);
+    for (int j = 0; j < 4; ++j) {
+      const int row = 8 * wave + 2 * j + hh;
+      bdma16(rs, (unsigned)(row * krow) + 16u * (unsigned)(n32 ^ (row & 15)), lb + 2 * j * kRow);
     }
   };
-  // part i (0..3) of the DMAs of tile t into buffers buf: half i & 1 of K (i < 2) or of V (i >= 2)
-  auto dma_part = [&](int t, int buf, int i) {
-    const int j0 = 4 * (i & 1);
-    if (i < 2) dma_tile(kbase, krow, t, lds0 + kK0 + buf * kTileBytes, true, j0, j0 + 4);
-    else dma_tile(vbase, vrow, t, lds0 + kV0 + buf * kTileBytes, false, j0, j0 + 4);
+  // V^T tile t into buffer buf: the tile is stored as its LDS image; wave w moves bytes [4 KB w, +4 KB)
+  auto dma_v = [&](int t, int buf) {
+    const char* src = vtbase + (size_t)t * kTileBytes + 4096 * wave;
+    unsigned lb = lds0 + kV0 + buf * kTileBytes + 4096 * wave;
+    asm volatile("" : "+s"(lb));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(src, (unsigned)(1024 * j + 16 * lane), lb + 1024 * j);
   };
 
-#pragma unroll
-  for (int i = 0; i < 4; ++i) dma_part(t_begin, 0, i);
+  dma_k(t_begin, 0);
+  dma_v(t_begin, 0);
 
-  // Q fragments (B operand of S^T = K Q^T): lane supplies Q[query n][16*s + 8*hh + j], j = 0..7
-  X8 qf[16];
+  // Q fragments (B operand of S^T = K Q^T): lane supplies Q[query n][32 ks + 8 g + j], j = 0..7
+  X8 qf[8];
 #pragma unroll
-  for (int s = 0; s < 16; ++s) {
-    const int c = 16 * s + 8 * hh;
+  for (int ks = 0; ks < 8; ++ks) {
+    const int c = 32 * ks + 8 * g;
     X8 val = X8{};
     if (qvalid) {
       val = __builtin_bit_cast(X8, *reinterpret_cast<const u32x4*>(qbase + (long)qidx * p.sq[1] + c));
@@ -155,144 +147,136 @@ __global__ __launch_bounds__(f256::kThreads) void flash256_kernel(FlashParams p)
         val = pack8(y, (X8*)nullptr);
       }
     }
-    qf[s] = val;
+    qf[ks] = val;
   }
 
-  // ---- per-lane LDS read addresses
-  // K (A operand of S^T): row r = 32 mb + n, chunk 2k + hh, stored at chunk slot (2k + hh) ^ (n & 15)
-  //   = ((hh ^ n) & 1) + 2 ((k & 7) ^ ((n >> 1) & 7)) + 16 (k >> 3).
-  unsigned kad[8];
+  // ---- per-lane LDS read addresses; buffers, blocks and k-steps are instruction offsets (< 64 KB)
+  // K (A operand of S^T): block kb reads row 16 kb + n at chunk 4 ks + g, stored at (4 ks + g) ^ n =
+  // 16 (ks >> 2) + 4 ((ks & 3) ^ (n >> 2)) + (g ^ (n & 3)).
+  unsigned kad[4];
 #pragma unroll
-  for (int k7 = 0; k7 < 8; ++k7)
-    kad[k7] = opaque(lds0 + kK0 + n * kRow + 16 * ((hh ^ n) & 1) + 32 * (k7 ^ ((n >> 1) & 7)));
-  // V^T (A operand of O^T), transpose reads: source lane (4 s + c) of group g reads key row
-  // R0 + z (z = 4 (g >> 1) + s, R0 a multiple of 8) at columns 32 ob + 16 (g & 1) + 4 c .. +3; with the
-  // chunk swizzle the byte address is (R0 + z) 512 + 64 (ob ^ z) + 32 (g & 1) + 8 c.
-  unsigned vad[8];
-  {
-    const int z = 4 * (g >> 1) + (gi >> 2);
-#pragma unroll
-    for (int ob = 0; ob < 8; ++ob)
-      vad[ob] = opaque(lds0 + kV0 + z * kRow + 64 * (ob ^ z) + 32 * (g & 1) + 8 * (gi & 3));
-  }
-
-  // S^T = K(buffer buf) Q^T. K fragments are read kQkAhead k-steps ahead of their MFMAs; the scheduling
-  // groups keep that order (the compiler otherwise issues half of the reads right before their MFMAs).
-  auto qk = [&](int buf, f32x16* s, auto&& after_first_reads) {
-    __builtin_amdgcn_sched_barrier(0);
-    auto kread = [&](int k, int mb) {
-      return *(const lds_x8*)(size_t)(kad[k & 7] + buf * kTileBytes + mb * 32 * kRow + 256 * (k >> 3));
-    };
-    constexpr int R = kQkAhead + 1;
-    X8 kf[R][2];
-#pragma unroll
-    for (int k = 0; k < kQkAhead; ++k) {
-      kf[k][0] = kread(k, 0);
-      kf[k][1] = kread(k, 1);
-    }
-    after_first_reads();
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      if (k + kQkAhead < 16) {
-        kf[(k + kQkAhead) % R][0] = kread(k + kQkAhead, 0);
-        kf[(k + kQkAhead) % R][1] = kread(k + kQkAhead, 1);
-      }
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) s[mb] = mma32(kf[k % R][mb], qf[k], k == 0 ? f32x16{} : s[mb]);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kQkAhead, 0);  // LDS reads of the first k-steps
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      if (k + kQkAhead < 16) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // reads of k-step k + ahead
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                         // MFMAs of k-step k
-    }
-    __builtin_amdgcn_sched_barrier(0);
+  for (int j = 0; j < 4; ++j) kad[j] = opaque(lds0 + kK0 + n * kRow + 64 * (j ^ (n >> 2)) + 16 * (g ^ (n & 3)));
+  auto kread = [&](int buf, int kb, int ks) {
+    return *(const lds_x8*)(size_t)(kad[ks & 3] + buf * kTileBytes + kb * 16 * kRow + 256 * (ks >> 2));
   };
-
-  // scaled row max of tile t (log2 units), the keys past the end set to -inf first
-  auto tile_max = [&](int t, f32x16* s) {
-    if ((t << 6) + 64 > kend) {
+  // V^T (A operand of O^T): block db reads row 16 db + n at chunk 4 u + g (keys vtl::vt_key(4 u + g, j))
+  unsigned vad[2];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if ((t << 6) + 32 * mb + 8 * (e >> 2) + 4 * hh + (e & 3) >= kend) s[mb][e] = -INFINITY;
-    }
-    float mm = s[0][0];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mm = fmaxf(mm, s[mb][e]);
-    return max_with_partner32(mm * p.sc);
+  for (int u = 0; u < 2; ++u) vad[u] = opaque(lds0 + kV0 + n * kVRow + 16 * vtl::vt_pos(4 * u + g, n));
+  auto vread = [&](int buf, int db, int u) {
+    return *(const lds_x8*)(size_t)(vad[u] + buf * kTileBytes + db * 16 * kVRow);
   };
 
   float m_run = -INFINITY, l_run = 0.f;
-  // O^T starts as an MFMA on zero operands, so that every definition of it is an accumulation register
-  f32x16 o[8];
+  f32x4 o[16];
 #pragma unroll
-  for (int ob = 0; ob < 8; ++ob) o[ob] = mma32(X8{}, X8{}, f32x16{});
+  for (int db = 0; db < 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Step of tile t, whose K and V are in buffers buf.
+  // Step of tile t, whose K and V^T are in buffers buf.
   auto step = [&](int t, int buf) {
-    // tile t+1 into the other buffers, released by the barrier that ended the previous step; its 16
-    // DMAs per wave go out in four groups spread over the step, since a burst of them stalls the wave
-    const bool more = t + 1 < t_end;
-    auto dma_at = [&](int point) {
+    if (t + 1 < t_end) {  // tile t+1 into the other buffers, released by the barrier that ended step t-1
+      dma_k(t + 1, buf ^ 1);
+      dma_v(t + 1, buf ^ 1);
+    }
+    if (active) {
+      // S^T: lane holds key 16 kb + 4 g + i of the tile for query n in s[kb][i]. MFMA i (k-step i / 4,
+      // block i % 4) reads its K fragment kAhead MFMAs earlier; the scheduling groups hold that order
+      // (left alone, the compiler issues each read right before its MFMA and waits for it).
+      f32x4 s[4];
+      {
+        __builtin_amdgcn_sched_barrier(0);
+        X8 kf[32];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (kDmaAt[i] == point && more) dma_part(t + 1, buf ^ 1, i);
-    };
-    dma_at(0);
-    f32x16 s[2];
-    qk(buf, s, [&] { dma_at(4); });
-    dma_at(1);
-    X8 b[4], blo[4];
-    {
-      const float mt = tile_max(t, s);
+        for (int i = 0; i < kAhead; ++i) kf[i] = kread(buf, i & 3, i >> 2);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const int kb = i & 3, ks = i >> 2;
+          s[kb] = mma16(kf[i], qf[ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[kb]);
+          if (i + kAhead < 32) kf[i + kAhead] = kread(buf, (i + kAhead) & 3, (i + kAhead) >> 2);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, kAhead, 0);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (i + kAhead < 32) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // the first V^T fragments of P.V, read while the softmax runs
+      X8 vf[32];
+#pragma unroll
+      for (int i = 0; i < kAhead; ++i) vf[i] = vread(buf, i & 15, i >> 4);
+      if ((t << 6) + 64 > kend) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if ((t << 6) + 16 * kb + 4 * g + i >= kend) s[kb][i] = -INFINITY;
+      }
+      float mm = s[0][0];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mm = fmaxf(mm, s[kb][i]);
+      const float mt = max_over_rows16(mm) * p.sc;
       if (wave_any(mt > m_run + kSlack)) {
         const float m_new = fmaxf(m_run, mt);
         const float alpha = exp2_fast(m_run - m_new);
         l_run *= alpha;
-        f256_rescale(o, alpha);
+#pragma unroll
+        for (int db = 0; db < 16; ++db) o[db] *= alpha;
         m_run = m_new;
       }
+      // P, and its sum as the P.V product sees it: f16 sums the rounded P (v_dot2), so that the weights
+      // of the numerator and of the denominator are the same numbers; bf16 (P as hi + lo) the f32 P
       const float c = -m_run;
+      X8 b[2], blo[2];
       float lsum = 0.f;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 2; ++u) {
         float pv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          pv[j] = exp2_fast(fmaf(s[u >> 1][8 * (u & 1) + j], p.sc, c));
-          lsum += pv[j];
-        }
+        for (int j = 0; j < 8; ++j) pv[j] = exp2_fast(fmaf(s[2 * u + (j >> 2)][j & 3], p.sc, c));
         b[u] = pack8(pv, (X8*)nullptr);
-        if (kSplitP) {
+        if constexpr (kSplitP) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) pv[j] -= to_f32(b[u][j]);
+          for (int j = 0; j < 8; ++j) {
+            lsum += pv[j];
+            pv[j] -= to_f32(b[u][j]);
+          }
           blo[u] = pack8(pv, (X8*)nullptr);
+        } else {
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+          for (int j = 0; j < 8; j += 2)
+            lsum = __builtin_amdgcn_fdot2(h2{b[u][j], b[u][j + 1]}, h2{(f16)1.f, (f16)1.f}, lsum, false);
         }
       }
       l_run += lsum;
-    }
-    dma_at(2);
-    // O^T += V^T . P^T over the tile's 4 groups of 16 keys; in bf16, P is split into hi + lo terms
+      // O^T += V^T . P^T (MFMA i: block i % 16, fragment u = i / 16), each V^T fragment read kAhead
+      // MFMAs earlier; in bf16, P is split into hi + lo terms
+      {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (u == 2) dma_at(3);
+        for (int i = 0; i < 32; ++i) {
+          const int db = i & 15, u = i >> 4;
+          o[db] = mma16(vf[i], b[u], o[db]);
+          if (kSplitP) o[db] = mma16(vf[i], blo[u], o[db]);
+          if (i + kAhead < 32) vf[i + kAhead] = vread(buf, (i + kAhead) & 15, (i + kAhead) >> 4);
+        }
 #pragma unroll
-      for (int ob = 0; ob < 8; ++ob) {
-        const unsigned r0 = buf * kTileBytes + (32 * (u >> 1) + 16 * (u & 1)) * kRow;
-        const X8 a = join8<T>(lds_read_tr16_at(vad[ob] + r0), lds_read_tr16_at(vad[ob] + r0 + 8 * kRow));
-        o[ob] = mma32(a, b[u], o[ob]);
-        if (kSplitP) o[ob] = mma32(a, blo[u], o[ob]);
+        for (int i = 0; i < 32; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, kSplitP ? 2 : 1, 0);
+          if (i + kAhead < 32) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     wait_vm<0>();
     __syncthreads();
   };
 
-  // All of this wave's loads (tile t0, Q, RoPE tables) done. A compiler-visible wait, so that the
+  // All of this wave's loads (tile t_begin, Q, RoPE tables) done. A compiler-visible wait, so that the
   // compiler's own load tracking does not carry the Q loads into the loop.
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
   __syncthreads();
@@ -302,22 +286,19 @@ __global__ __launch_bounds__(f256::kThreads) void flash256_kernel(FlashParams p)
   }
 
   if (!active) return;
-  // lane holds O^T[32*ob + 8*a + 4*hh + b][query n]
-  const float l = sum_with_partner32(l_run);
+  // lane holds O^T[16 db + 4 g + i][query n]; the four row groups of a query hold parts of its sum
+  const float l = sum_over_rows16(l_run);
   if (!qvalid) return;
   if (p.nsplit == 1) {
     const float inv = 1.f / l;
     T* orow = reinterpret_cast<T*>(p.out) + bi * p.so[0] + head * p.so[2] + (long)qidx * p.so[1];
 #pragma unroll
-    for (int ob = 0; ob < 8; ++ob)
+    for (int db = 0; db < 16; ++db) {
+      typename Vec<T>::x4 w4;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int d0 = 32 * ob + 8 * a + 4 * hh;
-        typename Vec<T>::x4 w4;
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb) w4[bb] = from_f32<T>(o[ob][4 * a + bb] * inv);
-        *reinterpret_cast<typename Vec<T>::x4*>(orow + d0) = w4;
-      }
+      for (int i = 0; i < 4; ++i) w4[i] = from_f32<T>(o[db][i] * inv);
+      *reinterpret_cast<typename Vec<T>::x4*>(orow + 16 * db + 4 * g) = w4;
+    }
   } else {
     // partial O [split][bh][q][256] and (max, sum) [split][bh][q][2]: f16 stores O / sum (a convex
     // combination of f16 values of v, so it stays in range), bf16 the unnormalised O in f32
@@ -326,29 +307,18 @@ __global__ __launch_bounds__(f256::kThreads) void flash256_kernel(FlashParams p)
       const float inv = 1.f / l;
       f16* prow = reinterpret_cast<f16*>(p.opart) + row * 256;
 #pragma unroll
-      for (int ob = 0; ob < 8; ++ob)
+      for (int db = 0; db < 16; ++db) {
+        Vec<f16>::x4 w4;
 #pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const int d0 = 32 * ob + 8 * a + 4 * hh;
-          Vec<f16>::x4 w4;
-#pragma unroll
-          for (int bb = 0; bb < 4; ++bb) w4[bb] = (f16)(o[ob][4 * a + bb] * inv);
-          *reinterpret_cast<Vec<f16>::x4*>(prow + d0) = w4;
-        }
+        for (int i = 0; i < 4; ++i) w4[i] = (f16)(o[db][i] * inv);
+        *reinterpret_cast<Vec<f16>::x4*>(prow + 16 * db + 4 * g) = w4;
+      }
     } else {
       float* prow = p.opart + row * 256;
 #pragma unroll
-      for (int ob = 0; ob < 8; ++ob)
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const int d0 = 32 * ob + 8 * a + 4 * hh;
-          f32x4 w4;
-#pragma unroll
-          for (int bb = 0; bb < 4; ++bb) w4[bb] = o[ob][4 * a + bb];
-          *reinterpret_cast<f32x4*>(prow + d0) = w4;
-        }
+      for (int db = 0; db < 16; ++db) *reinterpret_cast<f32x4*>(prow + 16 * db + 4 * g) = o[db];
     }
-    if (hh == 0) {
+    if (g == 0) {
       float2 ml;
       ml.x = m_run;
       ml.y = l;
@@ -357,16 +327,31 @@ __global__ __launch_bounds__(f256::kThreads) void flash256_kernel(FlashParams p)
   }
 }
 
-// True when flash256_kernel takes this problem: head dim exactly 256 and per-tile byte offsets of K and
-// V (64 rows) inside the 32-bit range of a buffer descriptor.
+size_t flash256_vt_bytes(int b, int h, int lk, int d) {
+  if (d != 256) return 0;
+  return (size_t)b * h * ((lk + 63) / 64) * f256::kTileBytes;
+}
+
+// True when flash256_kernel takes this problem: head dim exactly 256, room for the V^T tiles, and
+// per-tile byte offsets of K (64 rows) inside the 32-bit range of a buffer descriptor.
 bool flash256_eligible(const FlashParams& p, int elem_bytes) {
   const long lim = 1L << 30;
-  return p.d == 256 && p.sk[1] >= 0 && p.sv[1] >= 0 && 64L * p.sk[1] * elem_bytes < lim &&
-         64L * p.sv[1] * elem_bytes < lim;
+  return p.d == 256 && p.vt != nullptr && p.sk[1] >= 0 && 64L * p.sk[1] * elem_bytes < lim;
+}
+
+long flash256_vt_blocks(const VtJob& j) { return (long)j.b * j.h * ((j.lk + 63) / 64) * 4; }
+
+hipError_t flash256_vt(const VtJob& j, hipStream_t stream) {
+  hipLaunchKernelGGL(flash256_vt_kernel, dim3((unsigned)flash256_vt_blocks(j)), dim3(256), 0, stream, j);
+  return hipGetLastError();
 }
 
 template <typename T>
 static hipError_t launch256(FlashParams p, bool ropeq, hipStream_t stream) {
+  if (!p.vt_ready) {
+    VtJob j{p.v, {p.sv[0], p.sv[1], p.sv[2]}, p.b, p.h, p.lk, p.vt};
+    if (const hipError_t e = flash256_vt(j, stream); e != hipSuccess) return e;
+  }
   auto kern = ropeq ? flash256_kernel<T, true> : flash256_kernel<T, false>;
   static std::atomic<unsigned long long> lds_done[2];  // opt-in to more than 64 KB of dynamic LDS
   if (const hipError_t e = lds_opt_in(lds_done[ropeq], (const void*)kern, f256::kLds); e != hipSuccess) return e;

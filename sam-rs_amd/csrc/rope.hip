@@ -13,13 +13,16 @@
 #include <algorithm>
 
 #include "flash_attn.hpp"
+#include "flash_vt.hpp"
 
 namespace samhip {
 
 // Rotation with shared table reads: a thread owns (batch*head, table row t, 8 columns), reads that
 // piece of the cos and sin tables once, and rotates every row r = t (mod trows), r < nrot, of both row
 // sets (the cross-attention keys use each table row 7 times, and the queries once more). The threads
-// past the rotation part copy the rows r >= nrot. Same arithmetic per element as rope_rows_one.
+// past the rotation part copy the rows r >= nrot. Workgroups past those of the rows (vt_blocks of
+// them) write a head-dim-256 attention call's V as transposed key tiles (flash_vt.hpp), so that the
+// call's preparation is one launch.
 template <typename T>
 __device__ __forceinline__ void rope_rotate_rows(const RopeJob& jb, long bhx, int t, int c8, int trows,
                                                  const float* cs, const float* sn) {
@@ -57,8 +60,13 @@ __device__ __forceinline__ void rope_rotate_rows(const RopeJob& jb, long bhx, in
 template <typename T>
 __global__ __launch_bounds__(256) void rope_shared_kernel(RopeJob a, RopeJob b, int d, const float* __restrict__ cos_t,
                                                           const float* __restrict__ sin_t, int trows, int tused,
-                                                          long nrt, long ncopy_a, long ncopy_b) {
+                                                          long nrt, long ncopy_a, long ncopy_b, VtJob vt,
+                                                          unsigned row_blocks) {
   typedef typename Vec<T>::x8 X8;
+  if (blockIdx.x >= row_blocks) {  // uniform per workgroup
+    flash256_vt_quarter(vt, (long)(blockIdx.x - row_blocks));
+    return;
+  }
   const long c = (long)blockIdx.x * 256 + threadIdx.x;
   const int cpr = d / 8;
   if (c < nrt) {
@@ -141,7 +149,7 @@ RopeJob rope_job(const void* x, const long* sx, void* out, const long* so, int b
 }
 
 hipError_t rope_rows2(int dtype, const RopeJob& a, const RopeJob* b, int d, const float* cos_t, const float* sin_t,
-                      int trows, hipStream_t stream) {
+                      int trows, hipStream_t stream, const VtJob* vt) {
   RopeJob none{};
   const RopeJob& jb = b ? *b : none;
   // the shared-table kernel: one thread per (batch*head, used table row, 8 columns), then one per 8
@@ -152,14 +160,16 @@ hipError_t rope_rows2(int dtype, const RopeJob& a, const RopeJob* b, int d, cons
   const long nrt = bh * tused * cpr;
   const long ncopy_a = (long)a.b * a.h * (a.l - a.nrot) * cpr, ncopy_b = (long)jb.b * jb.h * (jb.l - jb.nrot) * cpr;
   const long threads = nrt + ncopy_a + ncopy_b;
-  if (threads == 0) return hipSuccess;
-  const unsigned blocks = (unsigned)((threads + 255) / 256);
+  const unsigned row_blocks = (unsigned)((threads + 255) / 256);
+  const VtJob vj = vt ? *vt : VtJob{};
+  const unsigned blocks = row_blocks + (vt ? (unsigned)flash256_vt_blocks(*vt) : 0u);
+  if (blocks == 0) return hipSuccess;
   if (dtype == kF16)
     hipLaunchKernelGGL(rope_shared_kernel<f16>, dim3(blocks), dim3(256), 0, stream, a, jb, d, cos_t, sin_t, trows,
-                       tused, nrt, ncopy_a, ncopy_b);
+                       tused, nrt, ncopy_a, ncopy_b, vj, row_blocks);
   else
     hipLaunchKernelGGL(rope_shared_kernel<bf16>, dim3(blocks), dim3(256), 0, stream, a, jb, d, cos_t, sin_t, trows,
-                       tused, nrt, ncopy_a, ncopy_b);
+                       tused, nrt, ncopy_a, ncopy_b, vj, row_blocks);
   return hipGetLastError();
 }
 

@@ -261,13 +261,13 @@ int device_cus() {
 
 struct FlashPlan {
   int qblocks, nsplit, tps;
-  size_t partial_bytes, krot_bytes, qrot_bytes, total;
+  size_t partial_bytes, krot_bytes, qrot_bytes, vt_bytes, total;
 };
 
 size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Workspace: key-split partials, then (when keys are rotated) the rotated keys and room for the rotated
-// queries, both contiguous [b, l, h, d].
+// queries, both contiguous [b, l, h, d], then (head dim 256) V as transposed key tiles.
 FlashPlan plan_flash(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k) {
   FlashPlan pl;
   samhip::flash_plan(b, h, lq, lk, d, device_cus(), &pl.qblocks, &pl.nsplit, &pl.tps);
@@ -275,7 +275,8 @@ FlashPlan plan_flash(int dtype, int b, int lq, int lk, int h, int d, int n_rope_
   const size_t elem = dtype == 0 ? 4 : 2;
   pl.krot_bytes = n_rope_k > 0 ? round256((size_t)b * lk * h * d * elem) : 0;
   pl.qrot_bytes = n_rope_k > 0 ? round256((size_t)b * lq * h * d * elem) : 0;
-  pl.total = pl.partial_bytes + pl.krot_bytes + pl.qrot_bytes;
+  pl.vt_bytes = round256(samhip::flash256_vt_bytes(b, h, lk, d));
+  pl.total = pl.partial_bytes + pl.krot_bytes + pl.qrot_bytes + pl.vt_bytes;
   return pl;
 }
 
@@ -338,6 +339,7 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
   p.v = v;
   p.out = out;
   bool ropeq = n_rope_q > 0;
+  p.vt = pl.vt_bytes > 0 ? ws + pl.partial_bytes + pl.krot_bytes + pl.qrot_bytes : nullptr;
   if (n_rope_k > 0) {
     // keys, and the queries when they are rotated too, go into the workspace as contiguous [b, l, h, d]
     // copies, in one launch; the attention kernel then reads plain operands
@@ -348,8 +350,12 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
     contiguous_strides(sqr, lq, h, d);
     const samhip::RopeJob jk = samhip::rope_job(k, p.sk, kr, skr, b, lk, h, d, n_rope_k);
     const samhip::RopeJob jq = samhip::rope_job(q, p.sq, qr, sqr, b, lq, h, d, n_rope_q);
-    hipError_t e = samhip::rope_rows2(dtype, jk, ropeq ? &jq : nullptr, d, rope_cos, rope_sin, rope_rows, s);
+    // head dim 256: V's transposed key tiles are written by the same launch
+    const samhip::VtJob jv{v, {p.sv[0], p.sv[1], p.sv[2]}, b, h, lk, p.vt};
+    hipError_t e = samhip::rope_rows2(dtype, jk, ropeq ? &jq : nullptr, d, rope_cos, rope_sin, rope_rows, s,
+                                      p.vt ? &jv : nullptr);
     if (e != hipSuccess) return check_launch(e, "flash-attn (rotation)");
+    p.vt_ready = p.vt != nullptr;
     p.k = kr;
     for (int i = 0; i < 3; ++i) p.sk[i] = skr[i];
     if (ropeq) {

@@ -5,7 +5,9 @@ The oracle restates the reference's attention back ends on the same seeded input
 kernel dtype (as tests/kernels.rs:28-31 does): sdpa (sam3/nn.rs:26-34) for the [B, H, L, D] layout,
 the per-(batch, query, head) scalar attention for the [B, L, H, D] layout that flash_attn_cpu and
 candle_flash_attn take (kernels.rs:416-434), rope (sam3/video.rs:106-113) and RopeAttn's core
-(sam3/video.rs:129-145). Bars: f16/bf16 max-abs 2e-3 against the f32 oracle; RoPE bit-exact.
+(sam3/video.rs:129-145). Bars: f16/bf16 max-abs 2e-3 against the f32 oracle, measured beyond the
+output's own rounding where that rounding alone reaches the bar (bf16 |out| >= 0.5, f16 |out| >= 4;
+tests/parity.py); RoPE bit-exact.
 """
 import numpy as np
 import pytest
