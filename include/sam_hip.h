@@ -137,8 +137,8 @@ int sam_hip_bias_gelu(const void* y, const void* bias, void* out, int dtype, lon
  * f32 tables rope_cos / rope_sin [rope_rows, d] (table row = index % rope_rows), the other rows are
  * used as they are; n_rope_q = n_rope_k = 0 disables it (the tables may then be NULL).
  * Workspace: sam_hip_flash_attn_workspace_size() bytes of device memory (16-byte aligned), for the
- * key-split partial results and, when n_rope_k > 0, the rotated keys and queries; it may be NULL when
- * that size is 0. The size depends on the current device's CU count: query it on the device that runs
+ * key-split partial results, when n_rope_k > 0 the rotated keys and queries, and when d == 256 V as
+ * transposed key tiles; it may be NULL when that size is 0. The size depends on the current device's CU count: query it on the device that runs
  * the call.
  * Limits: d % 8 == 0, d <= 256; scale >= 0; pointers and strides 16-byte aligned; out must not
  * overlap k, v or the workspace. f32 is rejected (SAM_HIP_EDTYPE), as by the reference's GPU flash
@@ -157,9 +157,9 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
  * in the reference: its GPU flash attention allocates internally. The workspace comes from a fixed
  * array of SAM_HIP_FLASH_NOALLOC_MAX_BYTES bytes that the library holds on every GPU it runs on until
  * the process ends; a call whose sam_hip_flash_attn_workspace_size exceeds it fails with
- * SAM_HIP_EUNSUPPORTED (SAM 2.1 memory attention needs about 51 MB). The call itself allocates
- * nothing. All calls on one GPU share that array: calls on one stream are ordered and safe, calls that
- * overlap on one GPU (several streams or threads) race. Arguments and limits otherwise as
+ * SAM_HIP_EUNSUPPORTED (SAM 2.1 memory attention needs at most 65.3 MB on 256 CUs). The call itself
+ * allocates nothing. All calls on one GPU share that array: calls on one stream are ordered and safe,
+ * calls that overlap on one GPU (several streams or threads) race. Arguments and limits otherwise as
  * sam_hip_flash_attn.
  */
 #define SAM_HIP_FLASH_NOALLOC_MAX_BYTES (64L << 20)
