@@ -138,8 +138,8 @@ int sam_hip_bias_gelu(const void* y, const void* bias, void* out, int dtype, lon
  * used as they are; n_rope_q = n_rope_k = 0 disables it (the tables may then be NULL).
  * Workspace: sam_hip_flash_attn_workspace_size() bytes of device memory (16-byte aligned), for the
  * key-split partial results, when n_rope_k > 0 the rotated keys and queries, and when d == 256 V as
- * transposed key tiles; it may be NULL when that size is 0. The size depends on the current device's CU count: query it on the device that runs
- * the call.
+ * transposed key tiles; it may be NULL when that size is 0. The size depends on the current device's
+ * CU count: query it on the device that runs the call.
  * Limits: d % 8 == 0, d <= 256; scale >= 0; pointers and strides 16-byte aligned; out must not
  * overlap k, v or the workspace. f32 is rejected (SAM_HIP_EDTYPE), as by the reference's GPU flash
  * attention.
@@ -150,6 +150,21 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
                        const long* strides_o, float scale, const float* rope_cos, const float* rope_sin,
                        int rope_rows, int n_rope_q, int n_rope_k, void* workspace, long workspace_bytes,
                        void* stream);
+
+/*
+ * sam3::nn::sdpa with an additive mask (sam3/nn.rs:26-34, Some(mask)): the f16 / bf16 GPU counterpart of
+ *   out[b, i, h, :] = softmax_j(scale * q[b,i,h,:] . k[b,j,h,:] + mask[b, h, i, j]) . v[b, :, h, :]
+ * for its masked callers: the key-padding text mask of SAM 3's DETR encoder and decoder (sam3/detr.rs:55,
+ * 191, 272; additive [1, 1, 1, L], 0 or -inf) and TinyViT's attention biases (sam1/tinyvit.rs:216;
+ * [1, heads, N, N]). The mask has the element type of q and is read through 4 element strides (batch,
+ * head, query, key); a stride of 0 broadcasts that dimension. A query whose keys are all -inf gets NaN,
+ * as the reference's softmax gives. Operands, strides, workspace (sam_hip_flash_attn_workspace_size
+ * with n_rope_k = 0) and limits as sam_hip_flash_attn; no RoPE; the mask must be 2-byte aligned.
+ */
+int sam_hip_sdpa_mask(const void* q, const void* k, const void* v, const void* mask, void* out, int dtype, int b,
+                      int lq, int lk, int h, int d, const long* strides_q, const long* strides_k,
+                      const long* strides_v, const long* strides_mask, const long* strides_o, float scale,
+                      void* workspace, long workspace_bytes, void* stream);
 
 /*
  * sam_hip_flash_attn without a workspace argument, for callers that cannot allocate device memory

@@ -269,6 +269,45 @@ void oracle_sdpa(const float* q, const float* k, const float* v, float* out, int
   }
 }
 
+/* sam3/nn.rs:26-34 with Some(mask): s = (q k^T) * scale, then s.broadcast_add(mask) (:29-32), softmax
+ * over the keys, times v. The mask is read through element strides sm (batch, head, query, key); a
+ * stride of 0 broadcasts. A row whose keys are all -inf comes out NaN, as candle's softmax gives. */
+void oracle_sdpa_mask(const float* q, const float* k, const float* v, const float* mask, const long* sm, float* out,
+                      int b, int h, int lq, int lk, int d, int nthreads) {
+  const float scale = powf((float)d, -0.5f);
+  const long heads = (long)b * h;
+  const long tiles = (lq + ORACLE_TILE - 1) / ORACLE_TILE;
+#pragma omp parallel num_threads(threads_or_all(nthreads))
+  {
+    float* kt = (float*)malloc(sizeof(float) * (size_t)d * lk);
+    float* sc = (float*)malloc(sizeof(float) * (size_t)ORACLE_TILE * lk);
+    long cur = -1;
+#pragma omp for schedule(static)
+    for (long task = 0; task < heads * tiles; ++task) {
+      const long bh = task / tiles, t = task % tiles;
+      const long bi = bh / h, hi = bh % h;
+      const float* kb = k + bh * (long)lk * d;
+      if (bh != cur) {
+        for (int j = 0; j < lk; ++j)
+          for (int c = 0; c < d; ++c) kt[(long)c * lk + j] = kb[(long)j * d + c];
+        cur = bh;
+      }
+      const int r0 = (int)(t * ORACLE_TILE);
+      const int rows = lq - r0 < ORACLE_TILE ? lq - r0 : ORACLE_TILE;
+      oracle_gemm_rows(q + (bh * lq + r0) * (long)d, kt, sc, rows, d, lk);
+      for (int r = 0; r < rows; ++r) {
+        float* row = sc + (long)r * lk;
+        const float* mrow = mask + bi * sm[0] + hi * sm[1] + (long)(r0 + r) * sm[2];
+        for (int j = 0; j < lk; ++j) row[j] = row[j] * scale + mrow[(long)j * sm[3]];
+        softmax_div(row, lk);
+      }
+      oracle_gemm_rows(sc, v + bh * (long)lk * d, out + (bh * lq + r0) * (long)d, rows, lk, d);
+    }
+    free(kt);
+    free(sc);
+  }
+}
+
 void oracle_mha_blhd(const float* q, const float* k, const float* v, float* out, int b, int lq, int lk, int h, int d,
                      float scale, int nthreads) {
   const long e = (long)h * d;

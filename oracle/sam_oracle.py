@@ -44,6 +44,7 @@ def lib():
         L.oracle_deform_attn.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 7 + [_I, ctypes.c_int]
         L.oracle_deform_prep.argtypes = [_F] * 5 + [ctypes.c_int] * 6 + [_I, ctypes.c_int]
         L.oracle_sdpa.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 6
+        L.oracle_sdpa_mask.argtypes = [_F, _F, _F, _F, ctypes.POINTER(ctypes.c_long), _F] + [ctypes.c_int] * 6
         L.oracle_mha_blhd.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int]
         L.oracle_rope_tables.argtypes = [ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_float, _F, _F]
         L.oracle_rope.argtypes = [_F, _F, _F, _F, ctypes.c_long, ctypes.c_int]
@@ -205,14 +206,21 @@ def bf16_flash_attention(q, k, v, scale: float | None = None, nthreads: int = 0)
     return out
 
 
-def sdpa(q, k, v, nthreads: int = 0) -> np.ndarray:
-    """sam3/nn.rs:26-34 with mask None. q [B,H,Lq,D], k/v [B,H,Lk,D] -> [B,H,Lq,D]."""
+def sdpa(q, k, v, mask=None, nthreads: int = 0) -> np.ndarray:
+    """sam3/nn.rs:26-34. q [B,H,Lq,D], k/v [B,H,Lk,D] -> [B,H,Lq,D]; mask None, or an additive mask that
+    broadcasts to [B,H,Lq,Lk]."""
     q, k, v = _f32(q), _f32(k), _f32(v)
     b, h, lq, d = q.shape
     lk = k.shape[2]
     assert k.shape == (b, h, lk, d) and v.shape == k.shape
     out = np.empty_like(q)
-    lib().oracle_sdpa(_p(q), _p(k), _p(v), _p(out), b, h, lq, lk, d, nthreads)
+    if mask is None:
+        lib().oracle_sdpa(_p(q), _p(k), _p(v), _p(out), b, h, lq, lk, d, nthreads)
+        return out
+    m = _f32(mask)
+    mb = np.broadcast_to(m, (b, h, lq, lk))  # stride 0 on the broadcast dimensions
+    sm = (ctypes.c_long * 4)(*[st // 4 for st in mb.strides])
+    lib().oracle_sdpa_mask(_p(q), _p(k), _p(v), _p(m), sm, _p(out), b, h, lq, lk, d, nthreads)
     return out
 
 

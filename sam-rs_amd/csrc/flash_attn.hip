@@ -1,10 +1,11 @@
-// Mask-free flash attention for gfx950, f16 / bf16: out = softmax(scale * q k^T) v per (batch, head).
+// Flash attention for gfx950, f16 / bf16: out = softmax(scale * q k^T [+ mask]) v per (batch, head).
 //
 // The GPU counterpart of the reference's three attention back ends on [B, L, H, D] tensors:
 // candle_flash_attn::flash_attn(q, k, v, scale, false) (sam2/hiera.rs:143-151, sam3/nn.rs:65-71,
 // sam3/vision.rs:116-121), kernels::flash_attn_cpu (kernels.rs:910-915 -> cpu_gemm.rs:361-417) and
-// sam3::nn::sdpa with no mask (sam3/nn.rs:26-34, which SAM 2 memory attention calls through
-// RopeAttn::forward, sam3/video.rs:129-145). Any (batch, row, head) strides are accepted, so both the
+// sam3::nn::sdpa (sam3/nn.rs:26-34), without a mask (SAM 2 memory attention calls it that way through
+// RopeAttn::forward, sam3/video.rs:129-145) or with an additive one (SAM 3's DETR text mask, TinyViT's
+// attention biases), which the MASK instances add to the scaled scores. Any (batch, row, head) strides are accepted, so both the
 // [B, L, H, D] and the [B, H, L, D] layouts are read in place; the head dimension is contiguous.
 //
 // Work decomposition: one workgroup = NW waves = NW * 32 queries of one (batch, head) and one range of
@@ -34,6 +35,7 @@
 namespace samhip {
 
 constexpr float kFlashSlack = 8.0f;
+constexpr float kFlashLog2e = 1.4426950408889634f;
 
 template <typename T, int DP, int NW>
 struct FlashGeom {
@@ -64,7 +66,7 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c0, float s0
   y1 = x1 * c1 + x0 * s1;
 }
 
-template <typename T, int DP, int NW, bool ROPEQ>
+template <typename T, int DP, int NW, bool ROPEQ, bool MASK>
 __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
   typedef FlashGeom<T, DP, NW> FG;
   typedef typename Vec<T>::x8 X8;
@@ -234,12 +236,26 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
           for (int e = 0; e < 16; ++e)
             if ((t << 6) + 32 * mb + 8 * (e >> 2) + 4 * hh + (e & 3) >= kend) s_cur[mb][e] = -INFINITY;
       }
+      if constexpr (MASK) {
+        // sdpa's additive mask (sam3/nn.rs:29-32) joins the scaled scores in log2 units:
+        // s <- s * scale * log2(e) + mask * log2(e); the softmax below then takes s as it is
+        const T* mrow = reinterpret_cast<const T*>(p.mask) + bi * p.sm[0] + head * p.sm[1] +
+                        (long)(qvalid ? qidx : 0) * p.sm[2];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int key = (t << 6) + 32 * mb + 8 * (e >> 2) + 4 * hh + (e & 3);
+            const float mv = key < kend ? to_f32(mrow[(long)key * p.sm[3]]) : 0.f;
+            s_cur[mb][e] = fmaf(s_cur[mb][e], sc, mv * kFlashLog2e);
+          }
+      }
       float mm = s_cur[0][0];
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mm = fmaxf(mm, s_cur[mb][e]);
-      const float mt = max_with_partner32(mm * sc);
+      const float mt = max_with_partner32(MASK ? mm : mm * sc);
       if (wave_any(mt > m_run + kFlashSlack)) {
         const float m_new = fmaxf(m_run, mt);
         const float alpha = exp2_fast(m_run - m_new);
@@ -249,14 +265,17 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
         m_run = m_new;
       }
       qk(ks_base + ((i + 1) & 1) * KBUF, s_nxt);
-      const float c = -m_run;
+      // with a mask, whole tiles (a row's first ones included) can be -inf: m_run is still -inf there
+      const float c = MASK && m_run == -INFINITY ? 0.f : -m_run;
+      constexpr float one = 1.f;
+      const float scs = MASK ? one : sc;  // the masked scores are scaled already
       float lsum = 0.f;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         float pv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          pv[j] = exp2_fast(fmaf(s_cur[u >> 1][8 * (u & 1) + j], sc, c));
+          pv[j] = exp2_fast(fmaf(s_cur[u >> 1][8 * (u & 1) + j], scs, c));
           lsum += pv[j];
         }
         b[u] = pack8(pv, (X8*)nullptr);
@@ -326,7 +345,7 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
     // combination of f16 values of v, so it stays in range), bf16 the unnormalised O in f32
     const long row = ((long)split * p.b * p.h + bhi) * p.lq + qidx;
     if constexpr (__is_same(T, f16)) {
-      const float inv = 1.f / l;
+      const float inv = MASK && l == 0.f ? 0.f : 1.f / l;  // a split whose keys are all masked: 0, weight 0
       f16* prow = reinterpret_cast<f16*>(p.opart) + row * DP;
 #pragma unroll
       for (int ob = 0; ob < MBO; ++ob)
@@ -408,8 +427,10 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p) {
     float cm = mx;
 #pragma unroll
     for (int j = 0; j < 8; ++j) cm = fmaxf(cm, ml[j].x);
+    // a split (or padding slot) whose keys are all masked has max -inf and sum 0: it weighs exactly 0,
+    // also while every split so far is of that kind (mx = -inf), so that no -inf - -inf reaches exp2
     if (s0 > 0) {
-      const float r = exp2_fast(mx - cm);
+      const float r = mx == -INFINITY ? 0.f : exp2_fast(mx - cm);
       den *= r;
 #pragma unroll
       for (int k = 0; k < 8; ++k) acc[k] *= r;
@@ -417,7 +438,7 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p) {
     mx = cm;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float w = exp2_fast(ml[j].x - mx);
+      const float w = ml[j].x == -INFINITY ? 0.f : exp2_fast(ml[j].x - mx);
       const float wl = w * ml[j].y;
       den += wl;
       const float f = __is_same(T, f16) ? wl : w;
@@ -442,12 +463,15 @@ template <typename T, int DP, int NW>
 static hipError_t launch_flash(FlashParams p, bool ropeq, hipStream_t stream) {
   typedef FlashGeom<T, DP, NW> FG;
   hipError_t e;
-  if (DP == 256 && flash256_eligible(p, (int)sizeof(T))) {
+  if (DP == 256 && !p.mask && flash256_eligible(p, (int)sizeof(T))) {
     e = flash256_launch(__is_same(T, f16) ? kF16 : kBF16, p, ropeq, stream);
   } else {
-    auto kern = ropeq ? flash_fwd_kernel<T, DP, NW, true> : flash_fwd_kernel<T, DP, NW, false>;
-    static std::atomic<unsigned long long> lds_done[2];  // opt-in to more than 64 KB of dynamic LDS
-    e = lds_opt_in(lds_done[ropeq], (const void*)kern, (int)FG::LDS);
+    const int which = p.mask ? 2 : ropeq ? 1 : 0;  // a masked call has no RoPE
+    auto kern = which == 2   ? flash_fwd_kernel<T, DP, NW, false, true>
+                : which == 1 ? flash_fwd_kernel<T, DP, NW, true, false>
+                             : flash_fwd_kernel<T, DP, NW, false, false>;
+    static std::atomic<unsigned long long> lds_done[3];  // opt-in to more than 64 KB of dynamic LDS
+    e = lds_opt_in(lds_done[which], (const void*)kern, (int)FG::LDS);
     if (e != hipSuccess) return e;
     const long blocks = (long)p.b * p.h * p.qblocks * p.nsplit;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(FG::NT), FG::LDS, stream, p);

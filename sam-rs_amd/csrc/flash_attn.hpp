@@ -22,6 +22,8 @@ struct FlashParams {
   int rrows, nrq;
   void* vt;                    // head dim 256: V as transposed key tiles (flash_vt.hpp), flash256_vt_bytes
   int vt_ready;                // the tiles are already written (by the rotation launch)
+  const void* mask;            // additive mask (element type), or null; strides sm: batch, head, query, key
+  long sm[4];
 };
 
 // V of a head-dim-256 call, to be written as transposed key tiles at vt (flash_vt.hpp).

@@ -303,11 +303,12 @@ long sam_hip_flash_attn_workspace_size(int dtype, int b, int lq, int lk, int h, 
   return (long)plan_flash(dtype, b, lq, lk, h, d, n_rope_k).total;
 }
 
-int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, int dtype, int b, int lq, int lk, int h,
+// sam_hip_flash_attn, and sam_hip_sdpa_mask when mask is not null (no RoPE then).
+static int flash_entry(const void* q, const void* k, const void* v, void* out, int dtype, int b, int lq, int lk, int h,
                        int d, const long* strides_q, const long* strides_k, const long* strides_v,
                        const long* strides_o, float scale, const float* rope_cos, const float* rope_sin,
                        int rope_rows, int n_rope_q, int n_rope_k, void* workspace, long workspace_bytes,
-                       void* stream) {
+                       void* stream, const void* mask, const long* strides_mask) {
   if (!q || !k || !v || !out) return fail(SAM_HIP_EINVAL, "flash-attn: null pointer argument");
   int rc = check_flash_sizes(dtype, b, lq, lk, h, d);
   if (rc != SAM_HIP_OK) return rc;
@@ -327,6 +328,15 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
   if ((rc = get_strides(strides_k, p.sk, lk, h, d, elem, "k")) != SAM_HIP_OK) return rc;
   if ((rc = get_strides(strides_v, p.sv, lk, h, d, elem, "v")) != SAM_HIP_OK) return rc;
   if ((rc = get_strides(strides_o, p.so, lq, h, d, elem, "out")) != SAM_HIP_OK) return rc;
+  if (mask) {
+    if (!strides_mask) return fail(SAM_HIP_EINVAL, "sdpa-mask: the mask needs its 4 strides (batch, head, query, key)");
+    for (int i = 0; i < 4; ++i) {
+      if (strides_mask[i] < 0) return fail(SAM_HIP_EUNSUPPORTED, "sdpa-mask: mask strides must be non-negative");
+      p.sm[i] = strides_mask[i];
+    }
+    if ((reinterpret_cast<size_t>(mask) & 1) != 0) return fail(SAM_HIP_EUNSUPPORTED, "sdpa-mask: mask must be 2-byte aligned");
+    p.mask = mask;
+  }
   const FlashPlan pl = plan_flash(dtype, b, lq, lk, h, d, n_rope_k);
   if (pl.total > 0 && (!workspace || workspace_bytes < (long)pl.total))
     return fail(SAM_HIP_EINVAL, "flash-attn: needs a workspace of %zu bytes (sam_hip_flash_attn_workspace_size), got %ld",
@@ -381,7 +391,26 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
   p.rsin = rope_sin;
   p.rrows = rope_rows;
   p.nrq = ropeq ? n_rope_q : 0;
-  return check_launch(samhip::flash_attn_half(dtype, p, ropeq, s), "flash-attn");
+  return check_launch(samhip::flash_attn_half(dtype, p, ropeq, s), mask ? "sdpa-mask" : "flash-attn");
+}
+
+int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, int dtype, int b, int lq, int lk, int h,
+                       int d, const long* strides_q, const long* strides_k, const long* strides_v,
+                       const long* strides_o, float scale, const float* rope_cos, const float* rope_sin,
+                       int rope_rows, int n_rope_q, int n_rope_k, void* workspace, long workspace_bytes,
+                       void* stream) {
+  return flash_entry(q, k, v, out, dtype, b, lq, lk, h, d, strides_q, strides_k, strides_v, strides_o, scale,
+                     rope_cos, rope_sin, rope_rows, n_rope_q, n_rope_k, workspace, workspace_bytes, stream, nullptr,
+                     nullptr);
+}
+
+int sam_hip_sdpa_mask(const void* q, const void* k, const void* v, const void* mask, void* out, int dtype, int b,
+                      int lq, int lk, int h, int d, const long* strides_q, const long* strides_k,
+                      const long* strides_v, const long* strides_mask, const long* strides_o, float scale,
+                      void* workspace, long workspace_bytes, void* stream) {
+  if (!mask) return fail(SAM_HIP_EINVAL, "sdpa-mask: null mask (use sam_hip_flash_attn for mask None)");
+  return flash_entry(q, k, v, out, dtype, b, lq, lk, h, d, strides_q, strides_k, strides_v, strides_o, scale, nullptr,
+                     nullptr, 0, 0, 0, workspace, workspace_bytes, stream, mask, strides_mask);
 }
 
 int sam_hip_rope(const void* x, const float* cos_t, const float* sin_t, void* out, int dtype, int b, int l, int h,

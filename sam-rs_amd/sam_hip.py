@@ -73,6 +73,8 @@ def load():
         L.sam_hip_flash_attn_noalloc.restype = _i
         L.sam_hip_rope.argtypes = [_vp] * 4 + [_i] * 5 + [_lp] * 2 + [_i, _i, _vp]
         L.sam_hip_rope.restype = _i
+        L.sam_hip_sdpa_mask.argtypes = [_vp] * 5 + [_i] * 6 + [_lp] * 5 + [_f, _vp, ctypes.c_long, _vp]
+        L.sam_hip_sdpa_mask.restype = _i
         _lib = L
     return _lib
 
@@ -357,13 +359,40 @@ def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float |
 
 
 def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask=None) -> torch.Tensor:
-    """sam3::nn::sdpa on [B, H, L, D] tensors: softmax(q k^T * D^-0.5) v. Only mask=None, the form
-    SAM 2 memory attention uses, runs on the GPU kernel; a mask raises."""
-    if mask is not None:
-        raise SamHipError("sdpa: the HIP flash kernel takes no additive mask")
+    """sam3::nn::sdpa on [B, H, L, D] tensors (sam3/nn.rs:26-34): softmax(q k^T * D^-0.5 + mask) v, with
+    an optional additive mask that broadcasts to [B, H, Lq, Lk] and has q's dtype, as candle's
+    broadcast_add needs. mask None goes through sam_hip_flash_attn, a mask through sam_hip_sdpa_mask."""
     d = q.shape[-1]
     out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    return _flash(q, k, v, out, "bhld", float(d) ** -0.5)
+    if mask is None:
+        return _flash(q, k, v, out, "bhld", float(d) ** -0.5)
+    for t in (q, k, v, mask):
+        if not t.is_cuda:
+            raise SamHipError("sam-rs HIP kernels need device tensors")
+    dt = _dtype(q, k, v)
+    if mask.dtype != q.dtype:
+        raise SamHipError(f"sdpa: the mask must have q's dtype {q.dtype}, got {mask.dtype}")
+    if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
+        raise SamHipError(f"sdpa: incompatible q/k/v shapes {tuple(q.shape)}/{tuple(k.shape)}/{tuple(v.shape)}")
+    b, h, lq, _ = q.shape
+    lk = k.shape[2]
+    if (k.shape[0], k.shape[1], k.shape[3]) != (b, h, d):
+        raise SamHipError(f"sdpa: incompatible q/k/v shapes {tuple(q.shape)}/{tuple(k.shape)}/{tuple(v.shape)}")
+    try:
+        m4 = mask.expand(b, h, lq, lk)  # broadcast dimensions get stride 0
+    except RuntimeError as e:
+        raise SamHipError(f"sdpa: mask {tuple(mask.shape)} does not broadcast to {(b, h, lq, lk)}") from e
+    L = load()
+    ws_bytes = L.sam_hip_flash_attn_workspace_size(dt, b, lq, lk, h, d, 0)
+    if ws_bytes < 0:
+        raise SamHipError(L.sam_hip_last_error().decode())
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    sm = (ctypes.c_long * 4)(*m4.stride())
+    rc = L.sam_hip_sdpa_mask(q.data_ptr(), k.data_ptr(), v.data_ptr(), m4.data_ptr(), out.data_ptr(), dt, b, lq, lk,
+                             h, d, _strides_blhd(q, "bhld"), _strides_blhd(k, "bhld"), _strides_blhd(v, "bhld"), sm,
+                             _strides_blhd(out, "bhld"), float(d) ** -0.5, ws.data_ptr(), ws_bytes, _stream())
+    _check(rc)
+    return out
 
 
 def _rope_tables(cos: torch.Tensor, sin: torch.Tensor, d: int, device):

@@ -161,15 +161,17 @@ def deform_prep64(off, logits, refs, shapes):
     return loc.numpy(), attn.numpy()
 
 
-def sdpa64(q, k, v, scale: float | None = None) -> np.ndarray:
-    """torch scaled_dot_product_attention in float64 on [..., L, D] tensors."""
+def sdpa64(q, k, v, scale: float | None = None, attn_mask=None) -> np.ndarray:
+    """torch scaled_dot_product_attention in float64 on [..., L, D] tensors; a float attn_mask is added to
+    the scaled scores."""
     import torch
     import torch.nn.functional as F
 
     qt = torch.as_tensor(np.asarray(q, np.float64))
     kt = torch.as_tensor(np.asarray(k, np.float64))
     vt = torch.as_tensor(np.asarray(v, np.float64))
-    return F.scaled_dot_product_attention(qt, kt, vt, scale=scale).numpy()
+    mt = None if attn_mask is None else torch.as_tensor(np.asarray(attn_mask, np.float64))
+    return F.scaled_dot_product_attention(qt, kt, vt, attn_mask=mt, scale=scale).numpy()
 
 
 def axial_rope_cis64(side: int, hd: int, theta: float) -> np.ndarray:

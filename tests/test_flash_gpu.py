@@ -62,6 +62,67 @@ def test_sdpa_bhld_layout(hip, b, h, lq, lk, d, dtype):
     check(got.float().cpu().numpy(), oracle.sdpa(q, k, v), dtype, f"sdpa {b}x{h}x{lq}x{lk}x{d} {dtype}")
 
 
+def masked_inputs(r, kind, b, h, lq, lk, d, dtype):
+    q, k, v = (rounded(r, (b, h, n, d), dtype) for n in (lq, lk, lk))
+    if kind == "bias":  # TinyViT's attention biases, one [N, N] table per head (sam1/tinyvit.rs:216)
+        mask = oracle.round_to(r.standard_normal((1, h, lq, lk)).astype(np.float32), dtype)
+    else:  # a key-padding mask of 0 / -inf per batch (sam3/detr.rs:55, 191, 272)
+        mask = np.zeros((b, 1, 1, lk), np.float32)
+        for bi in range(b):
+            mask[bi, ..., lk - 5 - 3 * bi:] = -np.inf
+    return q, k, v, mask
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("kind,b,h,lq,lk,d", [("bias", 3, 4, 49, 49, 32), ("padding", 2, 8, 200, 37, 32),
+                                              ("padding", 1, 2, 100, 130, 256), ("bias", 1, 2, 70, 300, 64),
+                                              ("padding", 2, 3, 33, 65, 128)])
+def test_sdpa_additive_mask(hip, kind, b, h, lq, lk, d, dtype):
+    """sdpa with Some(mask) (sam3/nn.rs:26-34): the mask broadcasts from its own shape (stride 0 on the
+    broadcast dimensions), is added to the scaled scores, and -inf drops a key."""
+    r = np.random.default_rng(11 + lk + d)
+    q, k, v, mask = masked_inputs(r, kind, b, h, lq, lk, d, dtype)
+    print(f"sdpa mask {kind} b={b} h={h} lq={lq} lk={lk} d={d} {dtype}", flush=True)
+    got = hip.sdpa(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype), to_dev(mask, dtype))
+    torch.cuda.synchronize()
+    check(got.float().cpu().numpy(), oracle.sdpa(q, k, v, mask), dtype, f"sdpa mask {kind} {b}x{h}x{lq}x{lk}x{d}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("where", ["tail", "head"])
+def test_sdpa_mask_whole_key_splits_masked(hip, where, dtype):
+    """One query block and 3000 keys split across many workgroups (16 splits of 3 tiles), with every key
+    past 150 ("tail") or before 2850 ("head") at -inf: most splits see only masked keys, and their
+    partials must weigh nothing in the combine, also when more than its first chunk of 8 splits is
+    masked. One query whose keys are all -inf comes out NaN, as the reference's softmax gives, and no
+    other row does."""
+    r = np.random.default_rng(5)
+    b, h, lq, lk, d = 1, 1, 40, 3000, 64
+    q, k, v = (rounded(r, (b, h, n, d), dtype) for n in (lq, lk, lk))
+    mask = np.zeros((1, 1, lq, lk), np.float32)
+    if where == "tail":
+        mask[..., 150:] = -np.inf
+    else:
+        mask[..., :2850] = -np.inf
+    mask[0, 0, 7, :] = -np.inf
+    got = hip.sdpa(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype), to_dev(mask, dtype))
+    torch.cuda.synchronize()
+    got = got.float().cpu().numpy()
+    want = oracle.sdpa(q, k, v, mask)
+    assert np.isnan(got[0, 0, 7]).all() and np.isnan(want[0, 0, 7]).all()
+    rows = [i for i in range(lq) if i != 7]
+    check(got[:, :, rows], want[:, :, rows], dtype, f"sdpa mask, split keys, {where} masked {dtype}")
+
+
+def test_sdpa_mask_rejects_bad_arguments(hip):
+    """A mask of another dtype, or one that does not broadcast to [B, H, Lq, Lk], is refused."""
+    q = torch.zeros(1, 2, 8, 32, device="cuda", dtype=torch.float16)
+    with pytest.raises(hip.SamHipError):
+        hip.sdpa(q, q, q, torch.zeros(1, 1, 1, 8, device="cuda", dtype=torch.float32))
+    with pytest.raises(hip.SamHipError):
+        hip.sdpa(q, q, q, torch.zeros(1, 3, 8, 8, device="cuda", dtype=torch.float16))
+
+
 def test_strided_views_are_read_in_place(hip):
     """A [B, L, H, D] slice of a wider packed projection (row stride > H*D) gives the same result as
     its contiguous copy."""

@@ -319,6 +319,60 @@ def test_sdpa_closed_forms(oracle_lib):
     assert np.abs(a - b).max() < 1e-6
 
 
+@pytest.mark.parametrize("mshape", ["bias", "padding", "query_rows"])
+def test_sdpa_mask_matches_torch_float64(oracle_lib, mshape):
+    """sdpa's additive mask (sam3/nn.rs:29-32) against torch's float64 SDPA with attn_mask, which adds the
+    mask to the scaled scores: TinyViT's per-head biases [1, H, N, N], DETR's key-padding mask
+    [B, 1, 1, Lk] of 0 / -inf, and a per-query [Lq, 1] column."""
+    r = _rng(16)
+    b, h, lq, lk, d = 2, 3, 19, 23, 32
+    q, k, v = (r.standard_normal((b, h, x, d)).astype(np.float32) for x in (lq, lk, lk))
+    if mshape == "bias":
+        mask = r.standard_normal((1, h, lq, lk)).astype(np.float32)
+    elif mshape == "padding":
+        mask = np.zeros((b, 1, 1, lk), np.float32)
+        mask[0, ..., 17:] = -np.inf
+        mask[1, ..., 3:9] = -np.inf
+    else:
+        mask = (2.0 * r.standard_normal((lq, 1))).astype(np.float32)
+    got = oracle_lib.sdpa(q, k, v, mask)
+    want = refimpl.sdpa64(q, k, v, attn_mask=np.broadcast_to(mask, (b, h, lq, lk)))
+    assert np.abs(got - want).max() < 2e-6
+
+
+def test_sdpa_mask_closed_forms(oracle_lib):
+    """A zero mask is no mask (bit for bit); a constant mask changes nothing (softmax is shift
+    invariant); -inf on a key set is the same as dropping those keys; a row with every key at -inf is
+    NaN, as candle's softmax gives, and leaves the other rows alone. A mask applied before the scale,
+    (s + m) * scale, a plausible slip that -inf masks cannot show, is far outside the float64
+    comparison's tolerance on a finite bias mask (checked here on the same inputs)."""
+    r = _rng(17)
+    b, h, lq, lk, d = 1, 2, 11, 13, 32
+    q, k, v = (r.standard_normal((b, h, x, d)).astype(np.float32) for x in (lq, lk, lk))
+    base = oracle_lib.sdpa(q, k, v)
+    assert np.array_equal(oracle_lib.sdpa(q, k, v, np.zeros((1, 1, 1, lk), np.float32)), base)
+    np.testing.assert_allclose(oracle_lib.sdpa(q, k, v, np.full((1, 1, 1, 1), 3.5, np.float32)), base, atol=2e-6)
+    keep = np.ones(lk, bool)
+    keep[[1, 4, 12]] = False
+    mask = np.where(keep, 0.0, -np.inf).astype(np.float32)[None, None, None, :]
+    np.testing.assert_allclose(oracle_lib.sdpa(q, k, v, mask), oracle_lib.sdpa(q, k[:, :, keep], v[:, :, keep]),
+                               atol=2e-6)
+    m = np.zeros((1, 1, lq, lk), np.float32)
+    m[0, 0, 5, :] = -np.inf
+    got = oracle_lib.sdpa(q, k, v, m)
+    assert np.isnan(got[:, :, 5]).all()
+    rows = [i for i in range(lq) if i != 5]
+    assert np.array_equal(got[:, :, rows], base[:, :, rows])
+    bias = r.standard_normal((1, h, lq, lk))
+    want = refimpl.sdpa64(q, k, v, attn_mask=bias)
+    s = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), k.astype(np.float64))
+    slip = (s + bias) * d ** -0.5
+    slip = np.exp(slip - slip.max(-1, keepdims=True))
+    slip = np.einsum("bhqk,bhkd->bhqd", slip / slip.sum(-1, keepdims=True), v.astype(np.float64))
+    assert np.abs(slip - want).max() > 1e-2
+    assert np.abs(oracle_lib.sdpa(q, k, v, bias.astype(np.float32)) - want).max() < 2e-6
+
+
 @pytest.mark.parametrize("b,lq,lk,h,d", [(1, 5, 7, 2, 16), (2, 17, 9, 3, 64)])
 def test_mha_blhd_matches_torch(oracle_lib, b, lq, lk, h, d):
     r = _rng(15)
