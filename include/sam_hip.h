@@ -39,6 +39,11 @@ enum sam_hip_status {
  * (sam1/encoder.rs:79-82; kernels.rs:12-43, 919-924, 1108-1149) and is the GPU counterpart of
  * attention_relpos_cpu (kernels.rs:899-906).
  * Limits: 1 <= h, w <= 64; hd % 8 == 0 and hd <= 128 (f16/bf16), hd % 4 == 0 and hd <= 128 (f32).
+ * Which kernel runs (f16/bf16) is chosen for speed only; every shape within the limits gets the same
+ * result to the same tolerance. Dedicated kernels take SAM's two shapes at hd 64 and 80: windows with
+ * 13 <= h <= 16 and an even w <= 16, and the 64-column global grid (w == 64, h <= 64) when
+ * 2^-6 <= scale * log2(e) <= 4 (SAM's hd^-0.5 * log2(e) is 0.16-0.18). Every other shape or scale runs
+ * on the general kernel, at a lower speed.
  */
 int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void* table, void* out, int dtype,
                         int bh, int h, int w, int hd, float scale, void* stream);
@@ -125,7 +130,7 @@ int sam_hip_bias_residual(const void* res, const void* y, const void* bias, void
 int sam_hip_bias_gelu(const void* y, const void* bias, void* out, int dtype, long total, int c, void* stream);
 
 /*
- * Flash attention without a mask, f16 / bf16, on [b, l, h, d] operands given by (batch, row, head)
+ * Flash attention without a mask, f32 / f16 / bf16, on [b, l, h, d] operands given by (batch, row, head)
  * element strides (NULL = contiguous [b, l, h, d]; the head dimension is always contiguous):
  *   out[b, i, h, :] = softmax_j(scale * q[b,i,h,:] . k[b,j,h,:]) . v[b, :, h, :]
  * Replaces the reference's GPU flash attention candle_flash_attn::flash_attn(q, k, v, scale, false)
@@ -140,9 +145,10 @@ int sam_hip_bias_gelu(const void* y, const void* bias, void* out, int dtype, lon
  * key-split partial results, when n_rope_k > 0 the rotated keys and queries, and when d == 256 V as
  * transposed key tiles; it may be NULL when that size is 0. The size depends on the current device's
  * CU count: query it on the device that runs the call.
+ * f32 is the reference's f32 GPU path (with --dtype f32 every attention runs as sdpa in candle's f32
+ * matmuls): exact f32 arithmetic in natural units, to 1e-5 relative of the exact result.
  * Limits: d % 8 == 0, d <= 256; scale >= 0; pointers and strides 16-byte aligned; out must not
- * overlap k, v or the workspace. f32 is rejected (SAM_HIP_EDTYPE), as by the reference's GPU flash
- * attention.
+ * overlap k, v or the workspace.
  */
 long sam_hip_flash_attn_workspace_size(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k);
 int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, int dtype, int b, int lq, int lk,
@@ -152,14 +158,14 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
                        void* stream);
 
 /*
- * sam3::nn::sdpa with an additive mask (sam3/nn.rs:26-34, Some(mask)): the f16 / bf16 GPU counterpart of
+ * sam3::nn::sdpa with an additive mask (sam3/nn.rs:26-34, Some(mask)), f32 / f16 / bf16:
  *   out[b, i, h, :] = softmax_j(scale * q[b,i,h,:] . k[b,j,h,:] + mask[b, h, i, j]) . v[b, :, h, :]
- * for its masked callers: the key-padding text mask of SAM 3's DETR encoder and decoder (sam3/detr.rs:55,
- * 191, 272; additive [1, 1, 1, L], 0 or -inf) and TinyViT's attention biases (sam1/tinyvit.rs:216;
- * [1, heads, N, N]). The mask has the element type of q and is read through 4 element strides (batch,
+ * the GPU counterpart for its masked callers: the key-padding text mask of SAM 3's DETR encoder and
+ * decoder (sam3/detr.rs:55, 191, 272; additive [1, 1, 1, L], 0 or -inf) and TinyViT's attention
+ * biases (sam1/tinyvit.rs:216; [1, heads, N, N]). The mask has the element type of q and is read through 4 element strides (batch,
  * head, query, key); a stride of 0 broadcasts that dimension. A query whose keys are all -inf gets NaN,
  * as the reference's softmax gives. Operands, strides, workspace (sam_hip_flash_attn_workspace_size
- * with n_rope_k = 0) and limits as sam_hip_flash_attn; no RoPE; the mask must be 2-byte aligned.
+ * with n_rope_k = 0) and limits as sam_hip_flash_attn; no RoPE; the mask is aligned to its element size.
  */
 int sam_hip_sdpa_mask(const void* q, const void* k, const void* v, const void* mask, void* out, int dtype, int b,
                       int lq, int lk, int h, int d, const long* strides_q, const long* strides_k,

@@ -27,7 +27,7 @@ SOURCES = [
     "bias_ops.hip",
     "relpos_softmax.hip",
     "qkv_split.hip",
-    "flash_attn.hip", "flash_attn_d256.hip", "flash_noalloc.hip",
+    "flash_attn.hip", "flash_attn_d256.hip", "flash_attn_f32.hip", "flash_noalloc.hip",
     "rope.hip",
     "sam_hip_abi.cpp",
 ]

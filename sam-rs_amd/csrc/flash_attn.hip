@@ -528,6 +528,25 @@ static hipError_t flash_dispatch(FlashParams p, bool ropeq, hipStream_t s) {
   }
 }
 
+template <int DP>
+static hipError_t combine_f32(FlashParams p, hipStream_t stream) {
+  const long rows = (long)p.b * p.h * p.lq;
+  constexpr int kRowsPerBlock = 256 / (DP / 8);
+  hipLaunchKernelGGL((flash_combine_kernel<float, DP>), dim3((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
+                     dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t flash_combine_f32(FlashParams p, int dp, hipStream_t stream) {
+  switch (dp) {
+    case 32: return combine_f32<32>(p, stream);
+    case 64: return combine_f32<64>(p, stream);
+    case 96: return combine_f32<96>(p, stream);
+    case 128: return combine_f32<128>(p, stream);
+    default: return combine_f32<256>(p, stream);
+  }
+}
+
 hipError_t flash_attn_half(int dtype, FlashParams p, bool ropeq, hipStream_t stream) {
   if (dtype == kF16) return flash_dispatch<f16>(p, ropeq, stream);
   return flash_dispatch<bf16>(p, ropeq, stream);

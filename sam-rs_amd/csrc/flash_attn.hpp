@@ -14,6 +14,7 @@ struct FlashParams {
   long sq[3], sk[3], sv[3], so[3];
   int b, h, lq, lk, d;
   float sc;                    // scale * log2(e)
+  float fscale;                // scale itself (the f32 kernel works in natural units, as the reference)
   int qblocks, nsplit, tps;    // query blocks, key splits, key tiles (of 64) per split
   float* opart;                // nsplit > 1: partial O [nsplit][b*h][lq][padded d]: f16 O / sum, or f32 O (bf16)
   float* ml;                   // nsplit > 1: running (max, sum) [nsplit][b*h][lq][2]
@@ -41,6 +42,9 @@ int flash_queries_per_block(int d);
 void flash_plan(int b, int h, int lq, int lk, int d, int cus, int* qblocks, int* nsplit, int* tps);
 size_t flash_partial_bytes(int b, int h, int lq, int d, int nsplit);
 hipError_t flash_attn_half(int dtype, FlashParams p, bool ropeq, hipStream_t stream);
+// f32 (flash_attn_f32.hip): the attention kernel and, with key splits, the combine.
+hipError_t flash_attn_f32(FlashParams p, bool ropeq, hipStream_t stream);
+hipError_t flash_combine_f32(FlashParams p, int dp, hipStream_t stream);
 // The head-dim-256 kernel (flash_attn_d256.hip): the bytes of its transposed V tiles, whether it takes
 // p, and its launch (the V tile pass and the main kernel; not the combine).
 size_t flash256_vt_bytes(int b, int h, int lk, int d);

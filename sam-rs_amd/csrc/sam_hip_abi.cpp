@@ -275,16 +275,13 @@ FlashPlan plan_flash(int dtype, int b, int lq, int lk, int h, int d, int n_rope_
   const size_t elem = dtype == 0 ? 4 : 2;
   pl.krot_bytes = n_rope_k > 0 ? round256((size_t)b * lk * h * d * elem) : 0;
   pl.qrot_bytes = n_rope_k > 0 ? round256((size_t)b * lq * h * d * elem) : 0;
-  pl.vt_bytes = round256(samhip::flash256_vt_bytes(b, h, lk, d));
+  pl.vt_bytes = dtype == 0 ? 0 : round256(samhip::flash256_vt_bytes(b, h, lk, d));
   pl.total = pl.partial_bytes + pl.krot_bytes + pl.qrot_bytes + pl.vt_bytes;
   return pl;
 }
 
 int check_flash_sizes(int dtype, int b, int lq, int lk, int h, int d) {
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
-  if (dtype == 0)
-    return fail(SAM_HIP_EDTYPE, "flash-attn: the MFMA flash kernel takes f16 or bf16 (the reference's GPU flash "
-                                "attention has the same limit); f32 attention goes through the CPU path");
   if (b <= 0 || lq <= 0 || lk <= 0 || h <= 0 || d <= 0)
     return fail(SAM_HIP_EINVAL, "flash-attn: sizes must be positive (b=%d lq=%d lk=%d h=%d d=%d)", b, lq, lk, h, d);
   if (d % 8 != 0 || d > 256)
@@ -334,7 +331,8 @@ static int flash_entry(const void* q, const void* k, const void* v, void* out, i
       if (strides_mask[i] < 0) return fail(SAM_HIP_EUNSUPPORTED, "sdpa-mask: mask strides must be non-negative");
       p.sm[i] = strides_mask[i];
     }
-    if ((reinterpret_cast<size_t>(mask) & 1) != 0) return fail(SAM_HIP_EUNSUPPORTED, "sdpa-mask: mask must be 2-byte aligned");
+    if ((reinterpret_cast<size_t>(mask) & (size_t)(elem - 1)) != 0)
+      return fail(SAM_HIP_EUNSUPPORTED, "sdpa-mask: the mask must be aligned to its element size");
     p.mask = mask;
   }
   const FlashPlan pl = plan_flash(dtype, b, lq, lk, h, d, n_rope_k);
@@ -350,7 +348,16 @@ static int flash_entry(const void* q, const void* k, const void* v, void* out, i
   p.out = out;
   bool ropeq = n_rope_q > 0;
   p.vt = pl.vt_bytes > 0 ? ws + pl.partial_bytes + pl.krot_bytes + pl.qrot_bytes : nullptr;
-  if (n_rope_k > 0) {
+  if (n_rope_k > 0 && dtype == 0) {
+    // f32: the keys go into the workspace rotated; the f32 kernel rotates the queries as it loads them
+    void* kr = ws + pl.partial_bytes;
+    long skr[3];
+    contiguous_strides(skr, lk, h, d);
+    hipError_t e = samhip::rope_rows(0, k, p.sk, kr, skr, b, lk, h, d, rope_cos, rope_sin, rope_rows, n_rope_k, s);
+    if (e != hipSuccess) return check_launch(e, "flash-attn (rotation)");
+    p.k = kr;
+    for (int i = 0; i < 3; ++i) p.sk[i] = skr[i];
+  } else if (n_rope_k > 0) {
     // keys, and the queries when they are rotated too, go into the workspace as contiguous [b, l, h, d]
     // copies, in one launch; the attention kernel then reads plain operands
     void* kr = ws + pl.partial_bytes;
@@ -380,6 +387,7 @@ static int flash_entry(const void* q, const void* k, const void* v, void* out, i
   p.lk = lk;
   p.d = d;
   p.sc = scale * 1.4426950408889634f;
+  p.fscale = scale;
   p.qblocks = pl.qblocks;
   p.nsplit = pl.nsplit;
   p.tps = pl.tps;
@@ -391,7 +399,8 @@ static int flash_entry(const void* q, const void* k, const void* v, void* out, i
   p.rsin = rope_sin;
   p.rrows = rope_rows;
   p.nrq = ropeq ? n_rope_q : 0;
-  return check_launch(samhip::flash_attn_half(dtype, p, ropeq, s), mask ? "sdpa-mask" : "flash-attn");
+  const hipError_t e = dtype == 0 ? samhip::flash_attn_f32(p, ropeq, s) : samhip::flash_attn_half(dtype, p, ropeq, s);
+  return check_launch(e, mask ? "sdpa-mask" : "flash-attn");
 }
 
 int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, int dtype, int b, int lq, int lk, int h,

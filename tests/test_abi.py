@@ -68,8 +68,8 @@ def test_flash_and_rope_argument_checks(lib):
                                      None, 0, 0, 0, None, 0, None)
     assert lib.sam_hip_flash_attn(None, None, None, None, 1, 1, 8, 8, 1, 64, None, None, None, None, 0.1, None,
                                   None, 0, 0, 0, None, 0, None) == 1
-    assert lib.sam_hip_flash_attn(*args(0, 64)) == 2
-    assert b"f16 or bf16" in lib.sam_hip_last_error()
+    assert lib.sam_hip_flash_attn(*args(3, 64)) == 2  # dtypes are 0, 1, 2
+    assert lib.sam_hip_flash_attn(*args(0, 20)) == 3  # f32 keeps the head-dim limits
     assert lib.sam_hip_flash_attn(*args(1, 20)) == 3
     assert lib.sam_hip_flash_attn(*args(1, 264)) == 3
     assert lib.sam_hip_flash_attn(*args(1, 64, -1.0)) == 1
@@ -77,6 +77,15 @@ def test_flash_and_rope_argument_checks(lib):
     # RoPE asked for without tables
     assert lib.sam_hip_flash_attn(fake, fake, fake, fake, 1, 1, 8, 8, 1, 64, None, None, None, None, 0.1, None, None,
                                   0, 8, 0, None, 0, None) == 1
+    # the masked sdpa: a null mask, missing or negative mask strides, a mask off its element alignment
+    lib.sam_hip_sdpa_mask.argtypes = [vp] * 5 + [i] * 6 + [lp] * 5 + [f, vp, ctypes.c_long, vp]
+    margs = lambda dt, mask, sm: (fake, fake, fake, mask, fake, dt, 1, 8, 8, 1, 64, None, None, None, sm, None, 0.1,
+                                  None, 0, None)
+    good = (ctypes.c_long * 4)(0, 0, 8, 1)
+    assert lib.sam_hip_sdpa_mask(*margs(1, None, good)) == 1
+    assert lib.sam_hip_sdpa_mask(*margs(1, fake, None)) == 1
+    assert lib.sam_hip_sdpa_mask(*margs(1, fake, (ctypes.c_long * 4)(0, 0, -8, 1))) == 3
+    assert lib.sam_hip_sdpa_mask(*margs(0, vp(0x1002), good)) == 3
     lib.sam_hip_rope.argtypes = [vp] * 4 + [i] * 5 + [lp] * 2 + [i, i, vp]
     assert lib.sam_hip_rope(fake, fake, fake, fake, 1, 1, 8, 1, 12, None, None, 8, 8, None) == 3
     assert lib.sam_hip_rope(fake, fake, fake, fake, 1, 1, 8, 1, 16, None, None, 8, 9, None) == 1

@@ -5,7 +5,8 @@ The oracle restates the reference's attention back ends on the same seeded input
 kernel dtype (as tests/kernels.rs:28-31 does): sdpa (sam3/nn.rs:26-34) for the [B, H, L, D] layout,
 the per-(batch, query, head) scalar attention for the [B, L, H, D] layout that flash_attn_cpu and
 candle_flash_attn take (kernels.rs:416-434), rope (sam3/video.rs:106-113) and RopeAttn's core
-(sam3/video.rs:129-145). Bars: f16/bf16 max-abs 2e-3 against the f32 oracle, measured beyond the
+(sam3/video.rs:129-145). Bars: f32 max|gpu - cpu| / max|cpu| <= 1e-5 (the reference's f32 GPU path is
+sdpa as candle matmuls); f16/bf16 max-abs 2e-3 against the f32 oracle, measured beyond the
 output's own rounding where that rounding alone reaches the bar (bf16 |out| >= 0.5, f16 |out| >= 4;
 tests/parity.py); RoPE bit-exact.
 """
@@ -40,7 +41,7 @@ BLHD = [(1, 5, 7, 2, 16), (2, 33, 65, 3, 64), (1, 40, 100, 1, 256), (2, 130, 200
         (2, 130, 517, 3, 256), (1, 70, 33, 2, 256), (1, 128, 64, 1, 256)]
 
 
-@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("b,lq,lk,h,d", BLHD)
 def test_flash_attn_matches_oracle(hip, b, lq, lk, h, d, dtype):
     r = np.random.default_rng(1000 + lq + lk + d)
@@ -51,7 +52,7 @@ def test_flash_attn_matches_oracle(hip, b, lq, lk, h, d, dtype):
     check(got.float().cpu().numpy(), want, dtype, f"flash_attn b{b} lq{lq} lk{lk} h{h} d{d} {dtype}")
 
 
-@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("b,h,lq,lk,d", [(1, 1, 5, 7, 16), (2, 3, 33, 65, 64), (1, 1, 40, 100, 256),
                                          (1, 2, 200, 700, 256)])
 def test_sdpa_bhld_layout(hip, b, h, lq, lk, d, dtype):
@@ -73,7 +74,7 @@ def masked_inputs(r, kind, b, h, lq, lk, d, dtype):
     return q, k, v, mask
 
 
-@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("kind,b,h,lq,lk,d", [("bias", 3, 4, 49, 49, 32), ("padding", 2, 8, 200, 37, 32),
                                               ("padding", 1, 2, 100, 130, 256), ("bias", 1, 2, 70, 300, 64),
                                               ("padding", 2, 3, 33, 65, 128)])
@@ -88,7 +89,7 @@ def test_sdpa_additive_mask(hip, kind, b, h, lq, lk, d, dtype):
     check(got.float().cpu().numpy(), oracle.sdpa(q, k, v, mask), dtype, f"sdpa mask {kind} {b}x{h}x{lq}x{lk}x{d}")
 
 
-@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("where", ["tail", "head"])
 def test_sdpa_mask_whole_key_splits_masked(hip, where, dtype):
     """One query block and 3000 keys split across many workgroups (16 splits of 3 tiles), with every key
@@ -227,7 +228,7 @@ def memory_inputs(side, frames, n_ptr, d, dtype, seed):
     return q, k, v, cos, sin
 
 
-@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("side,frames,n_ptr", [(8, 1, 0), (8, 3, 8), (6, 2, 4)])
 def test_rope_attention_small(hip, side, frames, n_ptr, dtype):
     """RopeAttn's attention core: self-attention (frames 1, no pointers) and cross-attention over tiled
@@ -250,7 +251,7 @@ def test_rope_attention_small(hip, side, frames, n_ptr, dtype):
         check(got[0].float().cpu().numpy(), want32, dtype, "rope_attention vs f32 rotation")
 
 
-@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("d,lq,n_rope_q", [(256, 200, 150), (64, 130, 130)])
 def test_rope_on_queries_only(hip, d, lq, n_rope_q, dtype):
     """Queries rotated and keys not (n_rope_k = 0): the rotation then happens while the attention kernel
@@ -312,8 +313,8 @@ def test_full_size_properties(hip):
 
 def test_flash_errors(hip):
     x16 = torch.zeros(1, 8, 1, 64, device="cuda", dtype=torch.float16)
-    with pytest.raises(hip.SamHipError, match="f16 or bf16"):
-        hip.flash_attn(x16.float(), x16.float(), x16.float())
+    with pytest.raises(hip.SamHipError, match="unsupported dtype"):
+        hip.flash_attn(x16.double(), x16.double(), x16.double())
     with pytest.raises(hip.SamHipError, match="multiple of 8"):
         y = torch.zeros(1, 8, 1, 20, device="cuda", dtype=torch.float16)
         hip.flash_attn(y, y, y)
