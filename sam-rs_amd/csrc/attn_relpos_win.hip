@@ -69,7 +69,8 @@ template <int HD> struct Shape {
   static constexpr int kQChunks = HD / 8;        // 16-byte chunks of a q or table row
   // Buffer b is a kT tile at 2 b kTile and a V tile right after it. The q rows fill buffer 1 and
   // the table the kT half of buffer 2 until the prologue has read them; a wave's bias scratch then
-  // overlays its own 32 q rows, which it alone reads (into registers) before it scatters.
+  // overlays its own 32 q rows, which it alone reads (into registers) before it scatters, and the
+  // same rows stage its output once the last tile is in buffer 0.
   static constexpr int kBuf = 2 * kTile;
   static constexpr int kQOff = kBuf;
   static constexpr int kTbOff = 2 * kBuf;
@@ -408,10 +409,14 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
       tile(3, 0, std::integral_constant<int, 1>());
   }
 
-  // ---- 4. normalise and store: lane holds O^T[32*ob + 8*a + 4*hh + b][query n]
-  const float inv = 1.f / sum_with_partner32(l_run);
-  if (qvalid) {
-    T* orow = out + u * unit_elems + qidx * HD;
+  // ---- 4. normalise and store: lane holds O^T[32*ob + 8*a + 4*hh + b][query n]. The wave's 32 output
+  // rows are consecutive in memory, so they go through LDS (its own q rows in buffer 1, free since the
+  // barrier before tile 3) as the [32][hd] image of that range and leave as contiguous 1 KB stores of
+  // 16-byte pieces. At hd 64 (128-byte rows) the 16-byte chunk c of row r sits at chunk c ^ (r & 7), so
+  // the 32 rows a store instruction covers spread over the banks.
+  if (active) {
+    const float inv = 1.f / sum_with_partner32(l_run);
+    T* stage = kring + S::kQOff + wave * 32 * HD;
 #pragma unroll
     for (int ob = 0; ob < kMBO; ++ob)
 #pragma unroll
@@ -420,9 +425,20 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
           typename Vec<T>::x4 w4;
 #pragma unroll
           for (int bb = 0; bb < 4; ++bb) w4[bb] = from_f32<T>(o[ob][4 * a + bb] * inv);
-          *reinterpret_cast<typename Vec<T>::x4*>(orow + 32 * ob + 8 * a + 4 * hh) = w4;
+          *reinterpret_cast<typename Vec<T>::x4*>(stage + n * HD + 8 * (HD == 64 ? (4 * ob + a) ^ (n & 7) : 4 * ob + a) + 4 * hh) = w4;
         }
       }
+    wave_sync();
+    const int q0w = q0 + wave * 32;
+    const int nbytes = min(32, N - q0w) * HD * (int)sizeof(T);  // valid rows only
+    char* dst = reinterpret_cast<char*>(out + u * unit_elems + (long)q0w * HD);
+    const char* src = reinterpret_cast<const char*>(stage);
+#pragma unroll
+    for (int i = 0; i < 32 * HD * (int)sizeof(T) / 1024; ++i) {
+      const int b = 1024 * i + 16 * lane;
+      const int sb = HD == 64 ? (b & ~127) + 16 * (((b >> 4) & 7) ^ ((b >> 7) & 7)) : b;
+      if (b < nbytes) *reinterpret_cast<u32x4*>(dst + b) = *reinterpret_cast<const u32x4*>(src + sb);
+    }
   }
 }
 
