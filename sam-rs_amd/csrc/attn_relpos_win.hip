@@ -14,21 +14,24 @@
 // and there are only 400 of them per ViT-H layer. So the kernel is built for overlap between
 // workgroups rather than for a single one:
 //   * a workgroup of 4 waves takes half a unit (query blocks 0-3 or 4-7, one per wave) and needs
-//     61 KB (hd 80) or 48 KB (hd 64) of LDS, so two (hd 80) or three (hd 64) fit on a CU: one loads
+//     80 KB (hd 80) or 48 KB (hd 64) of LDS, so two (hd 80) or three (hd 64) fit on a CU: one loads
 //     while another computes, and the 800 half units of a ViT-H layer fill the 512 workgroup slots of
 //     the chip in one and a half rounds instead of two full ones (the 600 of a ViT-B layer fit the 768
 //     slots at hd 64 in one);
 //   * all data moves by LDS DMA (global_load_lds): the q rows, the table and tile 0 are requested at
-//     once, q into ring buffer 1 and the table into buffer 2, which tiles 1 and 2 take over once the
-//     bias prologue has read them; tile 3 then goes into buffer 0. Both halves of a unit run on one
+//     once, q into ring buffer 1 and the table into buffer 2 (hd 80: into its own area), which tiles
+//     1 and 2 take over once the bias prologue has read them; tile 3 then goes into buffer 0. At hd 80
+//     the ring carries V only: the unit's whole kT is requested with the q rows, two contiguous rows
+//     per DMA, and stays resident (a tile's kT is 80 runs of 112 bytes at a 392-byte pitch, which
+//     costs more to fetch per tile than whole rows once). Both halves of a unit run on one
 //     XCD. In a grid of more than two rounds they are adjacent workgroups, so the second half's K and
 //     V come from L2. In a smaller grid all first halves go first, so that the last round holds the
 //     lighter second halves;
 //   * each wave waits only for its own DMAs of what it needs next (s_waitcnt vmcnt: a wave's vector
 //     memory operations complete in issue order), then one barrier publishes everyone's share;
-//   * kT tiles are stored [d][64 slots] with the 8-byte chunks of each row XOR-swizzled by the row's
-//     low bits, so the transpose reads (ds_read_b64_tr_b16) of four consecutive rows hit disjoint
-//     banks; V tiles are [64 slots][hd] with the 8-byte chunks of a slot rotated: hd 80 (160-byte
+//   * kT tiles are stored [d][64 slots] (hd 80: [d][4 tiles][64 slots], tile t in segment t ^ (d & 1))
+//     with the 8-byte chunks of each row XOR-swizzled by the row's low bits, so the transpose reads
+//     (ds_read_b64_tr_b16) of four consecutive rows hit disjoint banks; V tiles are [64 slots][hd] with the 8-byte chunks of a slot rotated: hd 80 (160-byte
 //     pitch) moves even slots by 4 chunks, hd 64 (128-byte pitch) slots 2, 3 (mod 4) by 8, so that the
 //     4 slots x 8 chunks of a half wave's transpose read fall on 64 distinct banks. hd 80: the O^T rows
 //     80..95 are discarded (their lanes re-read block 0). The softmax denominator is summed on the VALU;
@@ -67,20 +70,34 @@ template <int HD> struct Shape {
   static constexpr int kQDma = kQRows * HD * 2 / 1024 / kWaves;  // 1 KB units of q per wave: 5 or 4
   static constexpr int kChunks = HD / 4;         // 8-byte chunks of a V slot
   static constexpr int kQChunks = HD / 8;        // 16-byte chunks of a q or table row
-  // Buffer b is a kT tile at 2 b kTile and a V tile right after it. The q rows fill buffer 1 and
-  // the table the kT half of buffer 2 until the prologue has read them; a wave's bias scratch then
-  // overlays its own 32 q rows, which it alone reads (into registers) before it scatters, and the
-  // same rows stage its output once the last tile is in buffer 0.
-  static constexpr int kBuf = 2 * kTile;
-  static constexpr int kQOff = kBuf;
-  static constexpr int kTbOff = 2 * kBuf;
-  static constexpr size_t kLdsBytes = (size_t)kRing * kBuf * 2;
+  // Two layouts.
+  // * kRes (hd 80): the unit's whole kT is resident, [d][4 tiles][64 slots] at a 512-byte row pitch,
+  //   requested in the prologue by DMAs that each cover two whole rows of the unit's kT (two
+  //   contiguous 392-byte runs); only V goes through the ring (buffer b at kVOff + b kTile). The q rows
+  //   fill V buffers 1 and 2 until the prologue has read them; the table has its own area. 80 KB, two
+  //   workgroups per CU.
+  // * otherwise (hd 64): buffer b is a kT tile at 2 b kTile and a V tile right after it; the q rows
+  //   fill buffer 1 and the table the kT half of buffer 2 until the prologue has read them. 48 KB,
+  //   three workgroups per CU.
+  // In both, a wave's bias scratch then overlays its own 32 q rows, which it alone reads (into
+  // registers) before it scatters, and the same rows stage its output once the last tile is in
+  // buffer 0.
+  static constexpr bool kRes = HD == 80;
+  static constexpr int kSlots = kRes ? 256 : 64;   // kT row length in LDS (elements)
+  static constexpr int kBuf = kRes ? kTile : 2 * kTile;   // ring buffer stride
+  static constexpr int kVOff = kRes ? HD * 256 : kTile;   // V of ring buffer 0
+  static constexpr int kQOff = kRes ? kVOff + kTile : kBuf;
+  static constexpr int kTbOff = kRes ? kVOff + 3 * kTile : 2 * kBuf;
+  static constexpr int kKAll = kRes ? HD * 512 / 1024 / kWaves : 0;  // resident kT: DMAs per wave
+  static constexpr size_t kLdsBytes = kRes ? (size_t)(kTbOff + kTRows * HD) * 2 : (size_t)kRing * kBuf * 2;
+  static constexpr int kPerCU = kRes ? 2 : 3;       // workgroups per CU
   static_assert(HD == 80 || HD == 64, "head dims");
   static_assert(kRhsRows * 32 * sizeof(float) <= 32 * HD * 2, "the scratch fits in a wave's q rows");
-  static_assert((HD == 64 ? 3 : 2) * kLdsBytes <= 160 * 1024, "workgroups per CU");
+  static_assert(kPerCU * kLdsBytes <= 160 * 1024, "workgroups per CU");
   static_assert(kQRows * HD * 2 % (1024 * kWaves) == 0, "DMA split");
   static_assert(kTile * 2 <= kKDma * kWaves * 1024 && kTRows * HD * 2 <= kTbDma * kWaves * 1024, "units");
-  static_assert(kQRows * HD <= kBuf && kTRows * HD <= kTile, "staging fits buffers 1 and 2");
+  static_assert(kQRows * HD <= (kRes ? 2 * kTile : kBuf) && kTRows * HD <= kTile, "staging fits");
+  static_assert(!kRes || HD * 512 % (1024 * kWaves) == 0, "resident kT DMA split");
   // V chunk rotation: 8-byte chunk c of slot r is stored at (c + vrot(r)) % kChunks
   static constexpr int vrot(int r) { return HD == 80 ? ((r & 1) ? 0 : 4) : (((r >> 1) & 1) ? 8 : 0); }
   // q / table row rotation: 16-byte chunk c of LDS row r is stored at (c + qrot(r)) % kQChunks
@@ -153,16 +170,20 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   // rows past H read other keys of the unit (their bias is -inf, so P = 0) or, past the unit's end, 0
   const i32x4 krsrc = buffer_rsrc(kt + u * unit_elems, (unsigned)(sizeof(T) * unit_elems));
   const i32x4 vrsrc = buffer_rsrc(v + u * unit_elems, (unsigned)(sizeof(T) * unit_elems));
-  unsigned kdof[S::kKDma], vdof[S::kVDma];
+  constexpr int kKD = S::kRes ? S::kKAll : S::kKDma;
+  unsigned kdof[kKD], vdof[S::kVDma];
 #pragma unroll
-  for (int p = 0; p < S::kKDma; ++p) {
-    // kT: unit i covers rows 8i .. 8i+7 of the tile, a lane 16 bytes (8 slots) of row 8i + lane/8: the
-    // swizzle keeps 16-byte pairs of 8-byte chunks together, so they are the 8 consecutive slots
-    // from slot 4c = one grid row's columns kap .. kap+7 (kap = 0 or 8); hd 80: units 10, 11 repeat 0, 1
-    const int i = S::unit(wave + kWaves * p);
-    const int d = 8 * i + (lane >> 3);
+  for (int p = 0; p < kKD; ++p) {
+    // kT, 16 bytes (8 slots) a lane: the swizzle keeps 16-byte pairs of 8-byte chunks together, so they
+    // are the 8 consecutive slots from slot 4c = one grid row's columns kap .. kap+7 (kap = 0 or 8).
+    // Resident: unit i covers rows 2i, 2i+1, a lane row 2i + lane/32, segment (lane/8)%4, which holds
+    // tile t = segment ^ (d & 1). Ring: unit i covers rows 8i .. 8i+7 of the tile, a lane row
+    // 8i + lane/8 (the tile is the DMA's soffset); hd 80 would repeat units 0, 1 as 10, 11.
+    const int i = S::kRes ? wave * S::kKAll + p : S::unit(wave + kWaves * p);
+    const int d = S::kRes ? 2 * i + (lane >> 5) : 8 * i + (lane >> 3);
+    const int t = S::kRes ? ((lane >> 3) & 3) ^ (d & 1) : 0;
     const int c = (2 * (lane & 7)) ^ kswz(d & 3);
-    kdof[p] = (unsigned)(sizeof(T) * (d * N + (c >> 2) * W + 4 * (c & 3)));
+    kdof[p] = (unsigned)(sizeof(T) * (d * N + (4 * t + (c >> 2)) * W + 4 * (c & 3)));
   }
 #pragma unroll
   for (int p = 0; p < S::kVDma; ++p) {
@@ -175,15 +196,19 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
     vdof[p] = (unsigned)(sizeof(T) * (((slot >> 4) * W + (slot & 15)) * HD + col));
   }
 
-  // This wave's DMAs of K/V tile t (grid rows 4t .. 4t+3) into buffer buf (kTDma of them)
+  // This wave's DMAs of tile t (grid rows 4t .. 4t+3) into ring buffer buf: V, and kT unless it is
+  // resident (kTDma of them, or kVDma)
+  constexpr int kStepDma = S::kRes ? S::kVDma : kTDma;
   auto tile_dma = [&](int t, int buf) {
     const unsigned kso = (unsigned)(sizeof(T) * 4 * t * W), vso = kso * HD;
+    if constexpr (!S::kRes) {
 #pragma unroll
-    for (int p = 0; p < S::kKDma; ++p)
-      bdma16s(krsrc, kdof[p], kso, lds0 + (buf * kBuf + S::unit(wave + kWaves * p) * 512) * 2);
+      for (int p = 0; p < S::kKDma; ++p)
+        bdma16s(krsrc, kdof[p], kso, lds0 + (buf * kBuf + S::unit(wave + kWaves * p) * 512) * 2);
+    }
 #pragma unroll
     for (int p = 0; p < S::kVDma; ++p)
-      bdma16s(vrsrc, vdof[p], vso, lds0 + (buf * kBuf + kTile + S::unit(wave + kWaves * p) * 512) * 2);
+      bdma16s(vrsrc, vdof[p], vso, lds0 + (S::kVOff + buf * kBuf + S::unit(wave + kWaves * p) * 512) * 2);
   };
 
   // ---- 1. the half unit's q rows, the table and tile 0, all requested at once
@@ -213,17 +238,26 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
       dma16(base, (unsigned)(sizeof(T) * (src * HD + col)), lds0 + (S::kTbOff + i * 512) * 2);
     }
   }
+  if constexpr (S::kRes) {
+#pragma unroll
+    for (int p = 0; p < S::kKAll; ++p) bdma16s(krsrc, kdof[p], 0u, lds0 + (wave * S::kKAll + p) * 1024);
+  }
   tile_dma(0, 0);
 
   // per-lane constant parts of the transpose-read addresses
   // kT (A operand of S^T): source lane (4*s + c) of group g reads row 8*(g>>1) + s (+16*k, +4), the 4
   // slots slot(mb, 16*(g&1) + 4*c); the row's low bits are s, so the swizzle is lane constant
-  int koff[2];
+  // Resident kT: rows at a 512-byte pitch, tile t in segment t ^ (d & 1) (d & 1 is lane constant), so
+  // koff[0] serves even tiles (+ 64 t) and koff[1] odd ones; rows d and d + 1 still lie 32 banks
+  // apart, as in a 128-byte-pitch tile.
+  int koff[2][2];
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
     const int d = 8 * (g >> 1) + (gi >> 2);
     const int slot = KG::slot(mb, 16 * (g & 1) + 4 * (gi & 3));
-    koff[mb] = d * 64 + (((slot >> 2) ^ kswz(d & 3)) << 2);
+    const int base = d * S::kSlots + (((slot >> 2) ^ kswz(d & 3)) << 2);
+    koff[0][mb] = S::kRes ? base + 64 * (d & 1) : base;
+    koff[1][mb] = S::kRes ? base - 64 * (d & 1) : base;
   }
   // V^T (A operand of O^T): source lane (4*s + c) reads the slot of key 16*(w4&1) + 8*r + 4*(g>>1) + s of
   // block w4>>1, columns 32*ob + 16*(g&1) + 4*c .. +3 (logical chunk 8*ob + 4*(g&1) + c). hd 80: block
@@ -250,7 +284,7 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   };
 
   // ---- 2. the bias (q and the table have landed; tile 0 may still be in flight)
-  wait_vm<kTDma>();
+  wait_vm<S::kRes ? S::kKAll + S::kVDma : kTDma>();  // q and the table (kT, tile 0 may be in flight)
   __syncthreads();
   // this lane's q fragments (B operand of S^T = K Q^T): Q[query][16*s + 8*hh + j]
   X8 qf[kKS];
@@ -325,13 +359,13 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   auto tile = [&](int t, int buf, auto nb_c) {
     constexpr int NB = decltype(nb_c)::value;
     f32x16 s[2];
-    const T* kbuf = kring + buf * kBuf;
+    const T* kbuf = S::kRes ? kring + 64 * t : kring + buf * kBuf;
 #pragma unroll
     for (int mb = 0; mb < NB; ++mb) {
 #pragma unroll
       for (int k = 0; k < kKS; ++k) {
-        const T* p = kbuf + koff[mb] + 16 * k * 64;
-        const X8 a = join8<T>(lds_read_tr16(p), lds_read_tr16(p + 4 * 64));
+        const T* p = kbuf + koff[t & 1][mb] + 16 * k * S::kSlots;
+        const X8 a = join8<T>(lds_read_tr16(p), lds_read_tr16(p + 4 * S::kSlots));
         s[mb] = mma32(a, qf[k], k == 0 ? cinit : s[mb]);
       }
     }
@@ -373,7 +407,7 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
       }
     }
     l_run += lsum;
-    const T* vbuf = kring + buf * kBuf + kTile;
+    const T* vbuf = kring + S::kVOff + buf * kBuf;
 #pragma unroll
     for (int w4 = 0; w4 < 2 * NB; ++w4) {
 #pragma unroll
@@ -390,14 +424,14 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   // skips the key loop; it still moves its share of the tiles and takes part in every barrier.
   const bool active = q0 + wave * 32 < N;
   using Two = std::integral_constant<int, 2>;
-  wait_vm<2 * kTDma>();  // tile 0 (tiles 1, 2 may be in flight)
+  wait_vm<2 * kStepDma>();  // tile 0 (tiles 1, 2 may be in flight)
   __syncthreads();
   if (active) tile(0, 0, Two());
-  wait_vm<kTDma>();  // tile 1 (tile 2 may be in flight)
+  wait_vm<kStepDma>();  // tile 1 (tile 2 may be in flight)
   __syncthreads();
   tile_dma(3, 0);
   if (active) tile(1, 1, Two());
-  wait_vm<kTDma>();  // tile 2 (tile 3 may be in flight)
+  wait_vm<kStepDma>();  // tile 2 (tile 3 may be in flight)
   __syncthreads();
   if (active) tile(2, 2, Two());
   wait_vm<0>();  // tile 3
@@ -454,7 +488,7 @@ static hipError_t launch_win(const void* q, const void* kt, const void* v, const
   // When the grid fits in two rounds of the chip's workgroup slots, the second round should hold the
   // lighter second halves (68 of 196 queries at 14x14), so all first halves go first. Larger grids
   // keep the halves of a unit adjacent, so that the second half reads K and V from L2.
-  const long slots = (long)device_cu_count() * (HD == 64 ? 3 : 2);
+  const long slots = (long)device_cu_count() * win::Shape<HD>::kPerCU;
   const int n8 = bh <= slots ? (bh + 7) / 8 * 8 : 0;
   const unsigned grid = n8 > 0 ? (unsigned)(2 * n8) : (unsigned)(2 * bh);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(win::kThreads), lds, stream, (const T*)q, (const T*)kt, (const T*)v,
