@@ -8,8 +8,8 @@
 //
 // The work is streaming: each row is read once and written once (2 * N elements), so the kernel is
 // built around HBM traffic rather than arithmetic.
-//   * A wave owns 32 consecutive rows (16 for 16-bit rows of one vector per lane: the waves then cover
-//     twice as many rows in flight). Their bias dot products are one small GEMM, G = Table . Q^T
+//   * A wave owns 32 consecutive rows (16 for 16-bit rows of one vector per lane that the next kernel
+//     does not take: the waves then cover twice as many rows in flight). Their bias dot products are one small GEMM, G = Table . Q^T
 //     (all (2H-1) + (2W-1) table rows against the 32 q rows), on the MFMA (32x32x16 f16/bf16,
 //     32x32x2 f32), one 32-row block of the table at a time. Each lane then holds one q row's
 //     products with 16 table rows and scatters those that fall on the row's diagonal band into a
@@ -23,6 +23,8 @@
 //     groups ahead of the one being computed (a ring of three register buffers).
 //   * Rows that are not a multiple of 8 bytes, or that would need more than 16 vectors per lane, take a
 //     two-pass loop (online max and sum, then the outputs) over scalars.
+//   * 16-bit rows of at most 64 vectors (the 14x14 windows) take relpos_softmax_quad_kernel: 16 lanes
+//     per row, four rows per instruction, reductions inside a 16-lane group.
 // Arithmetic: the logit is (s * scale + Rh) + Rw with separate f32 roundings, as the reference's CPU
 // path computes it; exp(x - max) as exp2((x - max) * log2 e); P = e * (1 / sum).
 #include "common.hpp"
@@ -80,19 +82,19 @@ __device__ __forceinline__ typename Vec<T>::x8 load8(const T* row, int k, int le
   return r;
 }
 
-// The wave's bias rows: bias[row][0 .. W) = Rw, bias[row][W .. W+H) = Rh, row pitch bst floats (a
-// multiple of 4, so a row's Rw run can be read as 16-byte vectors). Lane l holds, per 32-row block tb of
-// the table, G[tb + m][row n] for m = 8 (e/4) + 4 (l/32) + e%4 (n = l % 32), the products of the wave's
-// q row n with table rows tb .. tb+31, and scatters those on the row's diagonal band.
+// The wave's bias rows: bias[row][0 .. W) = Rw, bias[row][rho .. rho+H) = Rh (rho >= W), row pitch bst
+// floats (a multiple of 4, so a row's Rw run can be read as 16-byte vectors). Lane l holds, per 32-row
+// block tb of the table, G[tb + m][row n] for m = 8 (e/4) + 4 (l/32) + e%4 (n = l % 32), the products of
+// the wave's q row n with table rows tb .. tb+31, and scatters those on the row's diagonal band.
 __device__ __forceinline__ void scatter_band(const f32x16& g, float* brow, int tb, int hh, int i, int j, int H,
-                                             int W) {
+                                             int W, int rho) {
   const int th = 2 * H - 1, trows = th + 2 * W - 1;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int tr = tb + 8 * (e >> 2) + 4 * hh + (e & 3);
     if (tr < th) {
       const int kh = i + H - 1 - tr;
-      if (kh >= 0 && kh < H) brow[W + kh] = g[e];
+      if (kh >= 0 && kh < H) brow[rho + kh] = g[e];
     } else if (tr < trows) {
       const int kw = j + W - 1 - (tr - th);
       if (kw >= 0 && kw < W) brow[kw] = g[e];
@@ -112,7 +114,7 @@ __device__ __forceinline__ void wave_sync() {
 // scattered).
 template <typename T>
 __device__ __forceinline__ void build_bias_short(const T* qrow, const T* tab, float* brow, int i, int j, int H, int W,
-                                                 int HD) {
+                                                 int HD, int rho) {
   const int lane = threadIdx.x & 63, n = lane & 31, hh = lane >> 5;
   const int trows = 2 * H - 1 + 2 * W - 1;
   if constexpr (__is_same(T, float)) {
@@ -139,7 +141,7 @@ __device__ __forceinline__ void build_bias_short(const T* qrow, const T* tab, fl
 #pragma unroll
       for (int t = 0; t < 64; ++t)
         if (t < half) g = __builtin_amdgcn_mfma_f32_32x32x2f32(tv[t], qv[t], g, 0, 0, 0);
-      scatter_band(g, brow, tb, hh, i, j, H, W);
+      scatter_band(g, brow, tb, hh, i, j, H, W, rho);
     }
   } else {
     typedef typename Vec<T>::x8 X8;
@@ -161,7 +163,7 @@ __device__ __forceinline__ void build_bias_short(const T* qrow, const T* tab, fl
 #pragma unroll
       for (int s = 0; s < 8; ++s)
         if (s < ks) g = mma32(a[s], qf[s], g);
-      scatter_band(g, brow, tb, hh, i, j, H, W);
+      scatter_band(g, brow, tb, hh, i, j, H, W, rho);
     }
   }
 }
@@ -169,7 +171,7 @@ __device__ __forceinline__ void build_bias_short(const T* qrow, const T* tab, fl
 // Any head dim (up to 256): one k-step at a time.
 template <typename T>
 __device__ __forceinline__ void build_bias_long(const T* qrow, const T* tab, float* brow, int i, int j, int H, int W,
-                                                int HD) {
+                                                int HD, int rho) {
   const int lane = threadIdx.x & 63, n = lane & 31, hh = lane >> 5;
   const int trows = 2 * H - 1 + 2 * W - 1;
   for (int tb = 0; tb < trows; tb += 32) {
@@ -186,13 +188,13 @@ __device__ __forceinline__ void build_bias_long(const T* qrow, const T* tab, flo
         g = mma32(load8(trow, k, HD, HD % 8 == 0), load8(qrow, k, HD, HD % 8 == 0), g);
       }
     }
-    scatter_band(g, brow, tb, hh, i, j, H, W);
+    scatter_band(g, brow, tb, hh, i, j, H, W, rho);
   }
 }
 
 template <typename T>
 __device__ __forceinline__ void build_bias(const T* q, const T* tab, float* bias, long r0, long rows, int H, int W,
-                                           int HD, int bst) {
+                                           int HD, int bst, int rho) {
   const int lane = threadIdx.x & 63, n = lane & 31;
   const int N = H * W;
   const long rq = min(r0 + n, rows - 1);
@@ -201,9 +203,9 @@ __device__ __forceinline__ void build_bias(const T* q, const T* tab, float* bias
   const T* qrow = q + rq * HD;
   float* brow = bias + n * bst;
   if (HD <= 128 && HD % 8 == 0)
-    build_bias_short(qrow, tab, brow, i, j, H, W, HD);
+    build_bias_short(qrow, tab, brow, i, j, H, W, HD, rho);
   else
-    build_bias_long(qrow, tab, brow, i, j, H, W, HD);
+    build_bias_long(qrow, tab, brow, i, j, H, W, HD, rho);
   wave_sync();
 }
 
@@ -339,7 +341,7 @@ __global__ __launch_bounds__(rsm::kWaves * 64) void relpos_softmax_vec_kernel(co
   RV b0[G][ITEMS], b1[G][ITEMS], b2[G][ITEMS];
   load_group(0, b0);
   if (G < nrows) load_group(G, b1);
-  build_bias(q, tab, bias, r0, rows, H, W, HD, bst);
+  build_bias(q, tab, bias, r0, rows, H, W, HD, bst, W);
   auto step = [&](int g0, RV (&cur)[G][ITEMS], RV (&spare)[G][ITEMS]) {
     if (g0 >= nrows) return;
     float x[G][ITEMS][VE], m[G];
@@ -352,6 +354,118 @@ __global__ __launch_bounds__(rsm::kWaves * 64) void relpos_softmax_vec_kernel(co
     step(g0, b0, b2);
     step(g0 + G, b1, b0);
     step(g0 + 2 * G, b2, b1);
+  }
+}
+
+// Short 16-bit rows (at most 64 vectors, W >= the vector's element count: the 14x14 windows' 196 keys
+// are 49 vectors of 8 bytes): 16 lanes per row, so one instruction covers four rows and a row's max and
+// sum take four DPP rotations inside its 16-lane group, with no permlane steps. A wave owns the 32 rows
+// of its bias block and runs them as 8 quads of rows.
+// Bias rows: Rw at [0, W) and repeated at [W, W + VE), so that a vector's VE Rw values are consecutive
+// even where it wraps into the next grid row; Rh at [W + VE, W + VE + H); one spare float after it.
+template <typename T, int VB, int VPL>
+__global__ __launch_bounds__(rsm::kWaves * 64) void relpos_softmax_quad_kernel(const T* __restrict__ s,
+                                                                              const T* __restrict__ q,
+                                                                              const T* __restrict__ tab,
+                                                                              T* __restrict__ out, long rows, int H,
+                                                                              int W, int HD, float scale, int bst) {
+#pragma clang fp contract(off)
+  using namespace rsm;
+  typedef typename Raw<T, VB>::type RV;
+  constexpr int VE = VB / (int)sizeof(T);
+  constexpr int kQuads = kRows / 4;
+  extern __shared__ float bias_lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long r0 = ((long)blockIdx.x * kWaves + wave) * kRows;
+  if (r0 >= rows) return;  // the waves of a workgroup share nothing
+  float* bias = bias_lds + wave * kRows * bst;
+  const int N = H * W, nvec = N / VE;
+  const int nrows = (int)min((long)kRows, rows - r0);
+  const int rq = lane >> 4, li = lane & 15;
+  RV raw[kQuads][VPL];
+  auto load_quad = [&](int qd) {
+    const int rl = 4 * qd + rq;
+    const T* srow = s + (r0 + (rl < nrows ? rl : 0)) * (long)N;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int v = li + 16 * j;
+      raw[qd][j] = v < nvec ? *reinterpret_cast<const RV*>(srow + v * VE) : RV{};
+    }
+  };
+  // Half the quads are requested before the bias prologue and half after it: all eight before it
+  // keep 196 registers live through the prologue's operands (two waves per SIMD, a second round of
+  // workgroups at the 14x14 window layer's 2450 waves), none before it leaves the first loads exposed.
+  constexpr int kPre = 4;
+#pragma unroll
+  for (int qd = 0; qd < kPre; ++qd) load_quad(qd);
+  const int rho = W + VE;
+  build_bias(q, tab, bias, r0, rows, H, W, HD, bst, rho);
+#pragma unroll
+  for (int qd = kPre; qd < kQuads; ++qd) load_quad(qd);
+  if (lane < 32) {
+#pragma unroll
+    for (int e = 0; e < VE; ++e) bias[lane * bst + W + e] = bias[lane * bst + e];
+  }
+  wave_sync();
+  // this lane's vectors: grid row and column of the first element, and the first element that lies in
+  // the next grid row (vectors past the row read row 0's bias and are discarded)
+  int kh0[VPL], kw0[VPL], wrap[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int v = li + 16 * j;
+    const int k = v < nvec ? v * VE : 0;
+    kh0[j] = k / W;
+    kw0[j] = k - kh0[j] * W;
+    wrap[j] = W - kw0[j];
+  }
+#pragma unroll
+  for (int qd = 0; qd < kQuads; ++qd) {
+    const int rl = 4 * qd + rq;
+    const float* brow = bias + min(rl, nrows - 1) * bst;
+    float x[VPL][VE];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const bool ok = li + 16 * j < nvec;
+      const float rh0 = brow[rho + kh0[j]], rh1 = brow[rho + kh0[j] + 1];
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        const float v = (raw_elem<T, VB>(raw[qd][j], e) * scale + (e < wrap[j] ? rh0 : rh1)) + brow[kw0[j] + e];
+        x[j][e] = ok ? v : -INFINITY;
+        m = fmaxf(m, x[j][e]);
+      }
+    }
+    m = fmaxf(m, row_ror<1>(m));
+    m = fmaxf(m, row_ror<2>(m));
+    m = fmaxf(m, row_ror<4>(m));
+    m = fmaxf(m, row_ror<8>(m));
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        x[j][e] = exp2_fast((x[j][e] - m) * kLog2e);
+        sum += x[j][e];
+      }
+    sum += row_ror<1>(sum);
+    sum += row_ror<2>(sum);
+    sum += row_ror<4>(sum);
+    sum += row_ror<8>(sum);
+    const float inv = 1.f / sum;
+    if (rl < nrows) {
+      T* orow = out + (r0 + rl) * (long)N;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        const int v = li + 16 * j;
+        if (v < nvec) {
+          typedef T TV __attribute__((ext_vector_type(VE)));
+          TV o;
+#pragma unroll
+          for (int e = 0; e < VE; ++e) o[e] = from_f32<T>(x[j][e] * inv);
+          *reinterpret_cast<TV*>(orow + v * VE) = o;
+        }
+      }
+    }
   }
 }
 
@@ -370,7 +484,7 @@ __global__ __launch_bounds__(rsm::kWaves * 64) void relpos_softmax_scalar_kernel
   const long r0 = ((long)blockIdx.x * kWaves + wave) * kRows;
   if (r0 >= rows) return;
   float* bias = bias_lds + wave * kRows * bst;
-  build_bias(q, tab, bias, r0, rows, H, W, HD, bst);
+  build_bias(q, tab, bias, r0, rows, H, W, HD, bst, W);
   const int N = H * W;
   const int nrows = (int)min((long)kRows, rows - r0);
   for (int rl = 0; rl < nrows; ++rl) {
@@ -437,6 +551,27 @@ static hipError_t launch_relpos_softmax(const void* s, const void* q, const void
   const size_t lds = (size_t)rsm::kWaves * rsm::kRows * bst * sizeof(float);
   const long row_bytes = (long)n * (long)sizeof(T);
   const int vb = row_bytes % 16 == 0 ? 16 : (row_bytes % 8 == 0 ? 8 : 0);
+  // 16-bit rows of at most 64 vectors whose vectors wrap at most once: 16 lanes per row
+  if constexpr (sizeof(T) == 2) {
+    if (vb && n / (vb / 2) <= 64 && w >= vb / 2) {
+      const int ve = vb / 2, nvec = n / ve;
+      const int bq = (w + ve + h + 1 + 3) / 4 * 4 + 4;
+      const size_t lq = (size_t)rsm::kWaves * rsm::kRows * bq * sizeof(float);
+      const int vpl = nvec <= 16 ? 1 : nvec <= 32 ? 2 : 4;
+      auto go = [&](auto kern) {
+        static std::atomic<unsigned long long> done{0};
+        if (const hipError_t e = lds_opt_in(done, (const void*)kern, (int)lq); e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(rsm::kWaves * 64), lq, stream, (const T*)s, (const T*)q,
+                           (const T*)tab, (T*)out, rows, h, w, hd, scale, bq);
+        return hipGetLastError();
+      };
+      if (vb == 16)
+        return vpl == 1 ? go(relpos_softmax_quad_kernel<T, 16, 1>)
+                        : vpl == 2 ? go(relpos_softmax_quad_kernel<T, 16, 2>) : go(relpos_softmax_quad_kernel<T, 16, 4>);
+      return vpl == 1 ? go(relpos_softmax_quad_kernel<T, 8, 1>)
+                      : vpl == 2 ? go(relpos_softmax_quad_kernel<T, 8, 2>) : go(relpos_softmax_quad_kernel<T, 8, 4>);
+    }
+  }
   if (vb) {
     const int ve = vb / (int)sizeof(T);
     const int nvec = n / ve;

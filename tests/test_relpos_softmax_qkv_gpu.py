@@ -37,10 +37,12 @@ def half_ulp_bf16(x):
 # The reference test's geometries, then shapes that take each of the kernel's paths: whole-row
 # 16-byte vectors (64-column grids, and 8192-long rows), 8-byte vectors (14x14 windows in f16), vectors
 # that straddle grid rows (33 and 14 columns), narrow grids (2 columns), the scalar two-pass kernel
-# (odd row lengths, and 8192 f32 columns), and row counts that leave a wave's 32 rows ragged.
+# (odd row lengths, and 8192 f32 columns), and row counts that leave a wave's 32 rows ragged. 16-bit
+# rows of at most 64 vectors run 16 lanes per row: one, two or four vectors per lane (64 columns;
+# 10x12 and 12x12 grids, whose 8-element vectors wrap into the next grid row; 14x14).
 RELPOS_SHAPES = [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (2, 3, 2, 8), (16, 33, 1, 32),
                  (64, 64, 2, 80), (14, 14, 40, 80), (13, 2, 5, 16), (5, 33, 3, 16), (128, 64, 1, 16),
-                 (91, 90, 1, 8), (1, 64, 7, 24)]
+                 (91, 90, 1, 8), (1, 64, 7, 24), (10, 12, 3, 16), (12, 12, 2, 16)]
 
 
 LONG_ROWS = {(128, 64, 1, 16), (91, 90, 1, 8)}  # f32 over ~8192 keys: test_relpos_softmax_long_rows_f32
