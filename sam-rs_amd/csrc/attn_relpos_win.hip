@@ -125,7 +125,7 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
                                                                        float scale, int nunits, int n8) {
   using namespace win;
   typedef Shape<HD> S;
-  constexpr int kKS = S::kKS, kMBO = S::kMBO, kTile = S::kTile, kBuf = S::kBuf, kTDma = S::kTDma;
+  constexpr int kKS = S::kKS, kMBO = S::kMBO, kBuf = S::kBuf, kTDma = S::kTDma;
   typedef KeyGeom<kPair> KG;
   typedef typename Vec<T>::x8 X8;
   constexpr bool kSplitP = __is_same(T, bf16);
