@@ -11,6 +11,7 @@
 // dimension is split in halves, hd index = (l / 32) * HDP/2 + step, so each lane's operands are
 // contiguous runs (vector LDS and global reads). The K tile is stored [slot][hd] (transposed from the
 // reference's kT while staging) and the V tile [slot][hd].
+#include "lds_dma.hpp"
 #include "relpos_geom.hpp"
 
 namespace samhip {
@@ -256,6 +257,206 @@ __global__ __launch_bounds__(NW * 64, (f32_min_blocks<HDP, MODE, NW>())) void at
   }
 }
 
+// ---------------------------------------------------------------------------------------------------
+// Windows at hd 64 (W <= 16, H * W <= 256: SAM ViT-B and ViT-L f32): a workgroup of 4 waves takes 128
+// queries of a unit (two per 14x14 window), every byte moves by 16-byte LDS DMA through a two-buffer
+// ring of 32-key tiles (two grid rows of 16 slots), and the workgroup needs 42 KB of LDS and at most
+// 168 registers, so three share a CU: the 600 workgroups of a ViT-B layer run in one round.
+//   * K tile: [d][32 slots] from kT rows, a 128-byte gap row between d < 32 and d >= 32, so that the two
+//     lane halves of an S^T step (dims s and 32 + s) read opposite halves of the banks;
+//   * V tile: [32 slots][64] with the 16-byte chunks of slots 16..31 rotated by 8, so that the two lane
+//     halves of a P.V step (slots e and 16 + e) read opposite halves of the banks;
+//   * S^T row m of a tile is slot 16 ((m >> 2) & 1) + 4 (m >> 3) + (m & 3): accumulator element e of lane
+//     (hh, n) is grid row hh of the tile, column e, so the Rw bias of element e is the same in every tile
+//     and the Rh bias is one value per lane and tile;
+//   * the logit is ((s * scale) + rh) + rw and P = expf(x - m), as in the kernel above.
+namespace f32w {
+constexpr int kWaves = 4, kThreads = 256, kHD = 64, kHalf = 32, kSlots = 32;
+constexpr int kKTile = (kHD + 1) * kSlots;   // floats: 64 rows and the gap row
+constexpr int kVTile = kSlots * kHD;
+constexpr int kBuf = kKTile + kVTile;
+constexpr int kRhs = 16 * 32;                // per-wave bias scratch: 16 rows (columns or grid rows) of 32
+constexpr size_t kLdsBytes = (size_t)(2 * kBuf + kWaves * kRhs) * sizeof(float);
+static_assert(3 * kLdsBytes <= 160 * 1024, "three workgroups per CU");
+__device__ __forceinline__ int slot_of_row(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
+}  // namespace f32w
+
+__global__ __launch_bounds__(f32w::kThreads, 3) void attn_relpos_f32_win_kernel(
+    const float* __restrict__ q, const float* __restrict__ kt, const float* __restrict__ v,
+    const float* __restrict__ table, float* __restrict__ out, int H, int W, float scale, int nunits, int halves) {
+  using namespace f32w;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* ring = reinterpret_cast<float*>(smem);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float* rhs = ring + 2 * kBuf + wave * kRhs;
+  const unsigned lds0 = lds_addr(smem);
+  const int lane = threadIdx.x & 63, n = lane & 31, hh = lane >> 5;
+  const int N = H * W;
+  // all first parts of the units go first, then the second parts (lighter at 14x14: 68 queries)
+  const long u = blockIdx.x % nunits;
+  const int part = blockIdx.x / nunits;
+  const int q0 = part * 128 + wave * 32;
+  const int qidx = q0 + n;
+  const bool qvalid = qidx < N;
+  const int qi = qvalid ? qidx / W : 0, qj = qvalid ? qidx - (qidx / W) * W : 0;
+  const long unit = (long)N * kHD;
+
+  // q fragments: lane supplies Q[query n][32 hh + s]
+  float qf[kHalf];
+#pragma unroll
+  for (int s = 0; s < kHalf; s += 4) {
+    f32x4 val = f32x4{};
+    if (qvalid) val = *reinterpret_cast<const f32x4*>(q + u * unit + (long)qidx * kHD + kHalf * hh + s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qf[s + i] = val[i];
+  }
+
+  // DMA offsets: wave w moves K units w and w + 4 (8 rows of 128 bytes each) and V units w and w + 4
+  // (4 slots of 256 bytes each); the tile's first key is the wave-uniform soffset
+  const i32x4 krsrc = buffer_rsrc(kt + u * unit, (unsigned)(sizeof(float) * unit));
+  const i32x4 vrsrc = buffer_rsrc(v + u * unit, (unsigned)(sizeof(float) * unit));
+  unsigned kdof[2], vdof[2], klds[2], vlds[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int ku = wave + 4 * p;
+    const int d = 8 * ku + (lane >> 3), piece = lane & 7;
+    kdof[p] = (unsigned)(sizeof(float) * ((long)d * N + (piece >> 2) * W + 4 * (piece & 3)));
+    klds[p] = (unsigned)(sizeof(float) * (ku < 4 ? ku * 256 : (ku * 256 + kSlots)));  // rows >= 32 after the gap
+    const int slot = 4 * ku + (lane >> 4), pos = lane & 15;
+    const int lc = (pos - 8 * (slot >> 4)) & 15;  // the logical chunk stored at position pos
+    vdof[p] = (unsigned)(sizeof(float) * (((slot >> 4) * W + (slot & 15)) * kHD + 4 * lc));
+    vlds[p] = (unsigned)(sizeof(float) * (kKTile + ku * 256));
+  }
+  auto tile_dma = [&](int t, int buf) {
+    const unsigned kso = (unsigned)(sizeof(float) * 2 * t * W), vso = kso * kHD;
+    const unsigned b = lds0 + (unsigned)(sizeof(float) * buf * kBuf);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) bdma16s(krsrc, kdof[p], kso, b + klds[p]);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) bdma16s(vrsrc, vdof[p], vso, b + vlds[p]);
+  };
+
+  // bias prologue: G = T . Q^T on the MFMA (table rows straight from memory), scattered along the
+  // diagonal band into this wave's scratch: Rw by key column, then Rh by key grid row
+  auto band = [&](const float* tab, int rows, int base, int len) {
+    for (int r0 = 0; r0 < rows; r0 += 32) {
+      f32x16 acc = {};
+      const int r = r0 + n;
+#pragma unroll
+      for (int s = 0; s < kHalf; s += 4) {
+        f32x4 a = f32x4{};
+        if (r < rows) a = *reinterpret_cast<const f32x4*>(tab + (long)r * kHD + kHalf * hh + s);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], qf[s + i], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int rr = r0 + 8 * (e >> 2) + 4 * hh + (e & 3);
+        const int k = base + len - 1 - rr;
+        if (rr < rows && k >= 0 && k < len) rhs[k * 32 + n] = acc[e];
+      }
+    }
+  };
+  const float* th = table;
+  const float* tw = table + (long)(2 * H - 1) * kHD;
+  const int ntiles = (H + 1) / 2;
+  tile_dma(0, 0);
+  band(tw, 2 * W - 1, qj, W);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float rw[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) rw[e] = e < W ? rhs[e * 32 + n] : -INFINITY;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  band(th, 2 * H - 1, qi, H);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  const unsigned kread = (unsigned)(sizeof(float) * (hh * (kHalf + 1) * kSlots + slot_of_row(n)));
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 o[2] = {f32x16{}, f32x16{}};
+  const bool active = q0 < N;  // a wave with no valid query moves its tile shares and skips the rest
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    wait_vm<0>();     // this wave's DMAs of tile t have landed
+    __syncthreads();  // everyone's tile t is visible; everyone is done with tile t - 1
+    if (t + 1 < ntiles) tile_dma(t + 1, buf ^ 1);
+    if (!active) continue;
+    const float* kb = reinterpret_cast<const float*>(smem + sizeof(float) * buf * kBuf + kread);
+    const float* vb = ring + buf * kBuf + kKTile;
+    f32x16 s = f32x16{};
+#pragma unroll
+    for (int st = 0; st < kHalf; ++st) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kb[st * kSlots], qf[st], s, 0, 0, 0);
+    const int row = 2 * t + hh;
+    const float rh = row < H ? rhs[row * 32 + n] : -INFINITY;
+    float mt = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float x = s[e] * scale;  // kernels.rs:202: x * scale + rh[kh] + rw[kw], left to right
+      x = x + rh;
+      x = x + rw[e];
+      s[e] = x;
+      mt = fmaxf(mt, x);
+    }
+    mt = max_with_partner32(mt);
+    if (wave_any(mt > m_run + kRescaleSlackNat)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = expf(m_run - m_new);
+      l_run *= alpha;
+      o[0] *= alpha;
+      o[1] *= alpha;
+      m_run = m_new;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pe = expf(s[e] - m_run);
+      s[e] = pe;
+      l_run += pe;
+    }
+    // O^T += V^T . P^T: step e pairs slot e (lanes hh = 0) with slot 16 + e (hh = 1)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float* vrow = vb + (16 * hh + e) * kHD;
+#pragma unroll
+      for (int ob = 0; ob < 2; ++ob) {
+        const int d = 32 * ob + n;
+        o[ob] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[4 * (((d >> 2) + 8 * hh) & 15) + (d & 3)], s[e], o[ob], 0, 0, 0);
+      }
+    }
+  }
+
+  const float inv = 1.f / sum_with_partner32(l_run);
+  if (qvalid) {
+    float* orow = out + u * unit + (long)qidx * kHD;
+#pragma unroll
+    for (int ob = 0; ob < 2; ++ob)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        f32x4 w4;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) w4[b] = o[ob][4 * a + b] * inv;
+        *reinterpret_cast<f32x4*>(orow + 32 * ob + 8 * a + 4 * hh) = w4;
+      }
+  }
+}
+
+static hipError_t launch_f32_win(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
+                                 int h, int w, float scale, hipStream_t stream) {
+  static std::atomic<unsigned long long> lds_done{0};
+  if (const hipError_t e = lds_opt_in(lds_done, (const void*)attn_relpos_f32_win_kernel, (int)f32w::kLdsBytes);
+      e != hipSuccess)
+    return e;
+  const int parts = (h * w + 127) / 128;
+  hipLaunchKernelGGL(attn_relpos_f32_win_kernel, dim3((unsigned)(bh * parts)), dim3(f32w::kThreads), f32w::kLdsBytes,
+                     stream, (const float*)q, (const float*)kt, (const float*)v, (const float*)table, (float*)out, h, w,
+                     scale, bh, parts);
+  return hipGetLastError();
+}
+
 template <int HDP, int MODE, int NW>
 static hipError_t launch_f32(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                              int hd, int h, int w, float scale, hipStream_t stream) {
@@ -301,6 +502,8 @@ hipError_t attn_relpos_f32(const void* q, const void* kt, const void* v, const v
                            int h, int w, float scale, hipStream_t stream) {
   if (hd <= 16) return f32_pick_mode<16>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   if (hd <= 32) return f32_pick_mode<32>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
+  if (hd == 64 && w <= 16 && h <= 16 && h * w <= 256)
+    return launch_f32_win(q, kt, v, table, out, bh, h, w, scale, stream);
   if (hd <= 64) return f32_pick_mode<64>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   if (hd <= 80) return f32_pick_mode<80>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   return f32_pick_mode<128>(q, kt, v, table, out, bh, hd, h, w, scale, stream);

@@ -45,14 +45,16 @@ def run_gpu(hip, arrays, h, w, scale, dtype):
 # grids with hd 80 and hd 64 of 1, 2, 3, 6 and 37 rows (ring shorter than its depth, odd tile counts, a
 # partial last query block); window grids with hd 80 and hd 64 of 13..16 rows (a full or half-empty
 # last key tile, idle query blocks), and narrow window grids of 2..8 columns, whose 8-slot DMA groups
-# span several grid rows.
+# span several grid rows; at hd 64 the f32 window kernel's one- to three-tile grids of fewer than 128
+# queries (3x7, 1x16, 5x9).
 SMALL = [(14, 14, 6, 64), (64, 64, 2, 64), (7, 11, 3, 80), (2, 3, 2, 8), (1, 5, 2, 16), (5, 33, 2, 32),
          (3, 40, 2, 128), (9, 17, 2, 48), (1, 64, 2, 80), (2, 64, 1, 80), (3, 64, 2, 80), (6, 64, 2, 80),
          (37, 64, 3, 80), (16, 16, 2, 80), (13, 12, 3, 80), (15, 14, 2, 80), (14, 10, 2, 80),
          (1, 64, 2, 64), (2, 64, 1, 64), (3, 64, 2, 64), (37, 64, 3, 64), (16, 16, 2, 64), (13, 12, 3, 64),
          (15, 14, 2, 64), (14, 10, 2, 64),
          (13, 2, 3, 80), (14, 4, 2, 80), (16, 6, 2, 80), (15, 8, 2, 80),
-         (13, 2, 3, 64), (14, 4, 2, 64), (16, 6, 2, 64), (15, 8, 2, 64)]
+         (13, 2, 3, 64), (14, 4, 2, 64), (16, 6, 2, 64), (15, 8, 2, 64),
+         (3, 7, 2, 64), (1, 16, 2, 64), (5, 9, 2, 64)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
