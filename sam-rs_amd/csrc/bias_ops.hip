@@ -2,7 +2,8 @@
 //   bias_residual: out = res + y + bias[col]                       (kernels.rs:618-640, sam.cu:129-134)
 //   bias_gelu:     out = gelu_erf(y + bias[col])                   (kernels.rs:642-663, sam.cu:136-141)
 // with col = index % c, the arithmetic in f32 in the reference's order ((res + y) + bias; x = y + bias,
-// then 0.5 * x * (1 + erf(x / sqrt(2)))) and one rounding to the output type.
+// then 0.5 * x * (1 + erf(x / sqrt(2))), the erf term through an erfc fit, see gelu_erf) and one
+// rounding to the output type.
 //
 // out may be res or y (in place): each element is read and then written by the same thread.
 // Both are bound by HBM: each thread moves 16-byte vectors of every operand (4 f32 or 8 f16/bf16
@@ -23,9 +24,28 @@ template <> struct Vec16<float> { typedef f32x4 type; static constexpr int n = 4
 template <> struct Vec16<f16> { typedef f16x8 type; static constexpr int n = 8; };
 template <> struct Vec16<bf16> { typedef bf16x8 type; static constexpr int n = 8; };
 
+// 0.5 x (1 + erf(x / sqrt 2)), with 1 + erf(x / sqrt 2) taken as erfc(|x| / sqrt 2) for x < 0 and
+// 2 - erfc(|x| / sqrt 2) otherwise, so that negative x loses nothing to cancellation. erfc is the
+// Chebyshev fit of Press et al., Numerical Recipes in C (2nd ed., section 6.2, erfcc): fractional
+// error below 1.2e-7 for every argument (1.04e-7 measured in float64 against the exact erfc; the f32
+// evaluation here stays within 7e-8 of the exact gelu in absolute terms). About 18 instructions
+// against some 45 for the device erff, which made this kernel arithmetic-bound.
 __device__ __forceinline__ float gelu_erf(float x) {
 #pragma clang fp contract(off)
-  return 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
+  const float z = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(1.f + 0.5f * z);
+  float p = 0.17087277f;
+  p = fmaf(t, p, -0.82215223f);
+  p = fmaf(t, p, 1.48851587f);
+  p = fmaf(t, p, -1.13520398f);
+  p = fmaf(t, p, 0.27886807f);
+  p = fmaf(t, p, -0.18628806f);
+  p = fmaf(t, p, 0.09678418f);
+  p = fmaf(t, p, 0.37409196f);
+  p = fmaf(t, p, 1.00002368f);
+  p = fmaf(t, p, -1.26551223f);
+  const float e = t * __builtin_amdgcn_exp2f(fmaf(-z, z, p) * 1.4426950408889634f);
+  return 0.5f * x * (x >= 0.f ? 2.f - e : e);
 }
 
 // MODE 0: bias_residual (res used), MODE 1: bias_gelu (res unused)
@@ -38,10 +58,16 @@ __global__ __launch_bounds__(bias::kThreads) void bias_ops_kernel(const T* res, 
     typedef typename Vec16<T>::type V;
     constexpr int n = Vec16<T>::n;
     const long nv = total / n;
-    for (long i = (long)blockIdx.x * bias::kThreads + threadIdx.x; i < nv; i += stride) {
+    // the bias column moves by the same amount every iteration: one 64-bit remainder per thread
+    long i = (long)blockIdx.x * bias::kThreads + threadIdx.x;
+    int col = (int)((i * n) % c);
+    const int step = (int)((stride * n) % c);
+    for (; i < nv; i += stride) {
       const long e = i * n;
       const V yv = *reinterpret_cast<const V*>(y + e);
-      const V bv = *reinterpret_cast<const V*>(b + (int)(e % c));
+      const V bv = *reinterpret_cast<const V*>(b + col);
+      col += step;
+      if (col >= c) col -= c;
       V o;
       if constexpr (MODE == 0) {
         const V rv = *reinterpret_cast<const V*>(res + e);
@@ -54,8 +80,13 @@ __global__ __launch_bounds__(bias::kThreads) void bias_ops_kernel(const T* res, 
       *reinterpret_cast<V*>(out + e) = o;
     }
   } else {
-    for (long i = (long)blockIdx.x * bias::kThreads + threadIdx.x; i < total; i += stride) {
-      const float bb = to_f32(b[(int)(i % c)]);
+    long i = (long)blockIdx.x * bias::kThreads + threadIdx.x;
+    int col = (int)(i % c);
+    const int step = (int)(stride % c);
+    for (; i < total; i += stride) {
+      const float bb = to_f32(b[col]);
+      col += step;
+      if (col >= c) col -= c;
       if constexpr (MODE == 0)
         out[i] = from_f32<T>(to_f32(res[i]) + to_f32(y[i]) + bb);
       else
