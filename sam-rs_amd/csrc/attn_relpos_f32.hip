@@ -457,6 +457,190 @@ static hipError_t launch_f32_win(const void* q, const void* kt, const void* v, c
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------------------
+// Global grids at hd 64 (W = 64: SAM ViT-B and ViT-L f32): 16 queries per wave on
+// v_mfma_f32_16x16x4_f32, a workgroup of 4 waves takes one grid row of 64 queries, so a ViT-B layer is
+// 12 x 64 = 768 workgroups: three per CU, three waves on every SIMD, one round. (With 32 queries per
+// wave the 12 heads x 4096 queries come in multiples of 64 queries per SIMD pair, and a quarter of the
+// CUs stayed idle.) K and V move by 16-byte LDS DMA through a two-buffer ring of 32-key tiles (half a
+// grid row); 48 KB of LDS.
+//   * lane (g, i) = (lane / 16, lane % 16) holds query i of its wave; S^T block kb (16 keys) element r is
+//     key 16 kb + 4 g + r; Q^T element s of the lane is dim 4 s + g;
+//   * K tile [d][32 keys] with the 4-key chunks of rows 2, 3 (mod 4) moved by 4 chunks, V tile
+//     [32 keys][64] with the 4-dim chunks of key k moved by 4 ((k >> 2) & 3) chunks: the four lane
+//     groups of a read fall on disjoint banks;
+//   * the Rw bias of element (kb, r) depends on the tile's half of the grid row only (16 values per
+//     lane), the Rh bias is one value per lane and grid row, kept in the wave's scratch;
+//   * the logit is ((s * scale) + rh) + rw and P = expf(x - m), as in the kernels above.
+namespace f32g {
+constexpr int kWaves = 4, kThreads = 256, kHD = 64, kSlots = 32;
+constexpr int kKTile = kHD * kSlots, kVTile = kSlots * kHD, kBuf = kKTile + kVTile;
+constexpr int kRhs = 64 * 16;  // per wave: [64 rows][16 queries]
+constexpr size_t kLdsBytes = (size_t)(2 * kBuf + kWaves * kRhs) * sizeof(float);
+static_assert(3 * kLdsBytes <= 160 * 1024, "three workgroups per CU");
+}  // namespace f32g
+
+__global__ __launch_bounds__(f32g::kThreads, 3) void attn_relpos_f32_glob16_kernel(
+    const float* __restrict__ q, const float* __restrict__ kt, const float* __restrict__ v,
+    const float* __restrict__ table, float* __restrict__ out, int H, float scale) {
+  using namespace f32g;
+  constexpr int W = 64;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* ring = reinterpret_cast<float*>(smem);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float* rhs = ring + 2 * kBuf + wave * kRhs;
+  const unsigned lds0 = lds_addr(smem);
+  const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
+  const int N = H * W;
+  // workgroups in contiguous ranges per XCD, so that the query rows of a head share an L2
+  const int total = (int)gridDim.x, per = total >> 3, rem = total & 7, xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int blk = xcd * per + (xcd < rem ? xcd : rem) + j;
+  const long bh = blk / H;
+  const int qi = blk % H, qj = 16 * wave + li;
+  const long unit = (long)N * kHD;
+  const float* qrow = q + bh * unit + (long)(qi * W + qj) * kHD;
+
+  float qf[16];  // Q^T[4 s + g][query]
+#pragma unroll
+  for (int s = 0; s < 16; ++s) qf[s] = qrow[4 * s + g];
+
+  // DMA: wave w moves K units w, w + 4 (rows 8u .. 8u+7, 128 bytes each) and V units w, w + 4 (keys
+  // 4u .. 4u+3, 256 bytes each) of a tile; the tile's first key is the wave-uniform soffset
+  const i32x4 krsrc = buffer_rsrc(kt + bh * unit, (unsigned)(sizeof(float) * unit));
+  const i32x4 vrsrc = buffer_rsrc(v + bh * unit, (unsigned)(sizeof(float) * unit));
+  unsigned kdof[2], vdof[2], klds[2], vlds[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int u = wave + 4 * p;
+    const int d = 8 * u + (lane >> 3), pos = lane & 7;
+    const int lc = pos ^ (4 * ((d >> 1) & 1));  // the 4-key chunk stored at position pos
+    kdof[p] = (unsigned)(sizeof(float) * ((long)d * N + 4 * lc));
+    klds[p] = (unsigned)(sizeof(float) * u * 256);
+    const int key = 4 * u + (lane >> 4), vpos = lane & 15;
+    const int vlc = vpos ^ (4 * ((key >> 2) & 3));
+    vdof[p] = (unsigned)(sizeof(float) * (key * kHD + 4 * vlc));
+    vlds[p] = (unsigned)(sizeof(float) * (kKTile + u * 256));
+  }
+  auto tile_dma = [&](int t, int buf) {
+    const unsigned kso = (unsigned)(sizeof(float) * kSlots * t), vso = kso * kHD;
+    const unsigned b = lds0 + (unsigned)(sizeof(float) * buf * kBuf);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) bdma16s(krsrc, kdof[p], kso, b + klds[p]);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) bdma16s(vrsrc, vdof[p], vso, b + vlds[p]);
+  };
+  const int ntiles = 2 * H;
+  tile_dma(0, 0);
+
+  // bias prologue: G = T . Q^T on the MFMA, 16 table rows per block (table rows straight from memory),
+  // scattered along the diagonal band: Rw into the scratch by key column, read into registers, then Rh
+  // by key grid row, which stays in the scratch
+  auto wsync = [&]() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  auto band = [&](const float* tab, int rows, int base, int len) {
+    for (int r0 = 0; r0 < rows; r0 += 16) {
+      const int r = min(r0 + li, rows - 1);
+      f32x4 acc = f32x4{};
+#pragma unroll
+      for (int s = 0; s < 16; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(tab[(long)r * kHD + 4 * s + g], qf[s], acc, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int rr = r0 + 4 * g + e;
+        const int k = base + len - 1 - rr;
+        if (rr < rows && k >= 0 && k < len) rhs[k * 16 + li] = acc[e];
+      }
+    }
+  };
+  band(table + (long)(2 * H - 1) * kHD, 2 * W - 1, qj, W);
+  wsync();
+  float rw[16];  // [tile half][kb][r]: key column 32 h + 16 kb + 4 g + r
+#pragma unroll
+  for (int e = 0; e < 16; ++e) rw[e] = rhs[(32 * (e >> 3) + 16 * ((e >> 2) & 1) + 4 * g + (e & 3)) * 16 + li];
+  wsync();
+  band(table, 2 * H - 1, qi, H);
+  wsync();
+
+  // per-lane LDS read offsets (floats): K row 4 s + g, key 16 kb + li (swizzled, one offset per kb); V
+  // key 16 kb + 4 g + r, dim 16 db + li (swizzled)
+  const int kofs0 = g * kSlots + (li ^ (16 * ((g >> 1) & 1)));
+  const int kofs1 = g * kSlots + ((16 + li) ^ (16 * ((g >> 1) & 1)));
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o[4] = {f32x4{}, f32x4{}, f32x4{}, f32x4{}};
+  // tile t is the half t & 1 of grid row t >> 1 and sits in ring buffer t & 1
+  auto step = [&](int t, auto half_c) {
+    constexpr int buf = decltype(half_c)::value;
+    wait_vm<0>();     // this wave's DMAs of tile t have landed
+    __syncthreads();  // everyone's tile t is visible; everyone is done with tile t - 1
+    if (t + 1 < ntiles) tile_dma(t + 1, buf ^ 1);
+    const float* kb0 = ring + buf * kBuf + kofs0;
+    const float* kb1 = ring + buf * kBuf + kofs1;
+    const float* vb = ring + buf * kBuf + kKTile;
+    f32x4 sacc[2] = {f32x4{}, f32x4{}};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      sacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb0[s * 4 * kSlots], qf[s], sacc[0], 0, 0, 0);
+      sacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb1[s * 4 * kSlots], qf[s], sacc[1], 0, 0, 0);
+    }
+    const float rh = rhs[(t >> 1) * 16 + li];
+    float x[8];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float y = sacc[e >> 2][e & 3] * scale;  // kernels.rs:202: x * scale + rh[kh] + rw[kw], left to right
+      y = y + rh;
+      y = y + rw[8 * buf + e];
+      x[e] = y;
+      mt = fmaxf(mt, y);
+    }
+    mt = max_over_rows16(mt);
+    if (wave_any(mt > m_run + kRescaleSlackNat)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = expf(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
+      m_run = m_new;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = expf(x[e] - m_run);
+      l_run += x[e];
+    }
+    // O^T += V^T . P^T: step (kb, r) pairs the keys 16 kb + 4 g + r of the four lane groups
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float* vrow = vb + (16 * (e >> 2) + 4 * g + (e & 3)) * kHD;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * (db ^ g) + li], x[e], o[db], 0, 0, 0);
+    }
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, std::integral_constant<int, 0>());
+    step(t + 1, std::integral_constant<int, 1>());
+  }
+
+  const float inv = 1.f / sum_over_rows16(l_run);
+  float* orow = out + bh * unit + (long)(qi * W + qj) * kHD;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = o[db] * inv;
+}
+
+static hipError_t launch_f32_glob16(const void* q, const void* kt, const void* v, const void* table, void* out,
+                                    int bh, int h, float scale, hipStream_t stream) {
+  static std::atomic<unsigned long long> lds_done{0};
+  if (const hipError_t e = lds_opt_in(lds_done, (const void*)attn_relpos_f32_glob16_kernel, (int)f32g::kLdsBytes);
+      e != hipSuccess)
+    return e;
+  hipLaunchKernelGGL(attn_relpos_f32_glob16_kernel, dim3((unsigned)(bh * h)), dim3(f32g::kThreads), f32g::kLdsBytes,
+                     stream, (const float*)q, (const float*)kt, (const float*)v, (const float*)table, (float*)out, h,
+                     scale);
+  return hipGetLastError();
+}
+
 template <int HDP, int MODE, int NW>
 static hipError_t launch_f32(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                              int hd, int h, int w, float scale, hipStream_t stream) {
@@ -504,6 +688,15 @@ hipError_t attn_relpos_f32(const void* q, const void* kt, const void* v, const v
   if (hd <= 32) return f32_pick_mode<32>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   if (hd == 64 && w <= 16 && h <= 16 && h * w <= 256)
     return launch_f32_win(q, kt, v, table, out, bh, h, w, scale, stream);
+  if (hd == 64 && w == 64) {
+    // 64 queries per workgroup, three per CU, against 256 queries per workgroup, one per CU: the
+    // former per round takes about 0.8 of the latter's round time (ViT-B, where each is one round),
+    // so it is taken unless it needs more rounds than that makes up for (ViT-L: 1024 workgroups are
+    // 1.33 rounds against one round of 256)
+    const long cus = device_cu_count(), g16 = (long)bh * h, g8 = (long)bh * ((h * 64 + 255) / 256);
+    const long rounds16 = (g16 + 3 * cus - 1) / (3 * cus), rounds8 = (g8 + cus - 1) / cus;
+    if (4 * rounds16 <= 5 * rounds8) return launch_f32_glob16(q, kt, v, table, out, bh, h, scale, stream);
+  }
   if (hd <= 64) return f32_pick_mode<64>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   if (hd <= 80) return f32_pick_mode<80>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
   return f32_pick_mode<128>(q, kt, v, table, out, bh, hd, h, w, scale, stream);

@@ -250,6 +250,19 @@ def test_vit_b_f32_layers(hip):
     check(got[heads], want, "f32", "vit-b global f32")
 
 
+def test_vit_l_f32_global_layer(hip):
+    """ViT-L f32 global layer (16 x 64x64, hd 64): its 1024 workgroups of 64 queries would take 1.33
+    rounds of the 16-queries-per-wave kernel, so it runs on the 32-queries-per-wave kernel; the oracle
+    checks heads 0, 8 and 15."""
+    print("vit-l f32 global", flush=True)
+    arrays = make_inputs(64, 64, 16, 64, 12, "f32", qkv_std=0.55)
+    got = run_gpu(hip, arrays, 64, 64, 0.125, "f32")
+    heads = [0, 8, 15]
+    q, kt, v, table = arrays
+    want = oracle.attention_relpos(q[heads], kt[heads], v[heads], table, 64, 64, 0.125)
+    check(got[heads], want, "f32", "vit-l global f32")
+
+
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_full_size_properties(hip, dtype):
     """Size-independent checks over every row of a batch-8 ViT-H global layer (BH 128): a constant
