@@ -43,7 +43,8 @@ enum sam_hip_status {
  * result to the same tolerance. Dedicated kernels take SAM's two shapes at hd 64 and 80: windows with
  * 13 <= h <= 16 and an even w <= 16, and the 64-column global grid (w == 64, h <= 64) when
  * 2^-6 <= scale * log2(e) <= 4 (SAM's hd^-0.5 * log2(e) is 0.16-0.18). Every other shape or scale runs
- * on the general kernel, at a lower speed.
+ * on the general kernel, at a lower speed. In f32, hd 64 has its own window kernel (w <= 16, h <= 16,
+ * h*w <= 256) and global kernel (w == 64); other f32 shapes run on the general f32 kernel.
  */
 int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void* table, void* out, int dtype,
                         int bh, int h, int w, int hd, float scale, void* stream);
