@@ -71,6 +71,31 @@ int sam_hip_qkv_split(const void* y, const void* bias, void* out, int dtype, lon
                       void* stream);
 
 /*
+ * qkv_split on the unpadded token grid, with the window partition in it:
+ *   y [batch*gh*gw, 3*nh*hd] (the qkv projection of the grid tokens, row (b*gh + r)*gw + c), bias as
+ *   above -> out [3, bh*n*hd] as sam_hip_qkv_split writes it for the windows of the grid zero-padded to
+ *   multiples of ws: n = ws*ws, bh = batch * ceil(gh/ws) * ceil(gw/ws) * nh, window (b, wi, wj) in that
+ *   order, token (ti, tj) of it at grid (wi*ws + ti, wj*ws + tj).
+ * The reference partitions the normalised tokens first (sam1/encoder.rs:129-137) and runs the qkv
+ * linear on the padded windows, so a padding token's projection is 0 and its q, k and v are the bias
+ * alone; this entry point writes exactly that, so the linear can run on the gh*gw grid tokens only.
+ * No reference entry point of its own: the composition of window_partition and kernels::qkv_split
+ * (kernels.rs:872-894). Limits: hd <= 256, ws <= 256, gh, gw <= 4096; 16-byte aligned pointers.
+ */
+int sam_hip_qkv_split_grid(const void* y, const void* bias, void* out, int dtype, int batch, int gh, int gw, int ws,
+                           int nh, int hd, void* stream);
+
+/*
+ * The attention output back on the grid: ctx [bh, ws*ws, hd] in the window order of
+ * sam_hip_qkv_split_grid -> out [batch, gh, gw, nh*hd], heads merged (the transpose and reshape of
+ * sam1/encoder.rs:83) and the windows put back without their padding (window_unpartition,
+ * sam1/encoder.rs:140-143). A copy: out holds ctx's values. No reference entry point of its own.
+ * Limits: ws <= 256, gh, gw <= 4096; 16-byte aligned pointers.
+ */
+int sam_hip_window_merge(const void* ctx, void* out, int dtype, int batch, int gh, int gw, int ws, int nh, int hd,
+                         void* stream);
+
+/*
  * Multi-scale deformable attention (Grounding DINO), forward:
  *   out[b, q, h*d + c] = sum_{l,p} attn[b,q,h,l,p] * bilinear(value_l[b,:,h,c], (x*W_l - 0.5, y*H_l - 0.5))
  * with (x, y) = loc[b,q,h,l,p,:], zero padding outside each level.

@@ -13,6 +13,17 @@
 // arithmetic has no division: q and v rows are copied with 16-byte accesses on both sides; the k part
 // goes through an LDS tile so that kT is written as rows of consecutive tokens (up to 128 bytes in
 // f16) rather than 2-byte scatters. Bound by HBM: y is read once, out written once.
+//
+// Grid mode (gw > 0): y holds the tokens of the unpadded [B, gh, gw] grid, and the windows are cut from
+// it here, as the reference's window_partition (sam1/encoder.rs:129-137) does before its qkv linear:
+// window w = (b, wi, wj) over the grid zero-padded to multiples of ws, token (ti, tj) of it at grid
+// (wi*ws + ti, wj*ws + tj). A padding token's projection is 0, so its q, k and v are the bias alone
+// (from_T(0 + bias), as the reference computes them). The qkv linear then runs on the gh*gw grid
+// tokens instead of the padded windows' ones.
+//
+// window_merge is the step after the attention: ctx [B*nW*nh, ws*ws, hd] in window order -> out
+// [B, gh, gw, nh*hd], heads merged (sam1/encoder.rs:83) and the windows put back on the grid without
+// their padding (window_unpartition, sam1/encoder.rs:140-143), one 16-byte vector per thread.
 #include "common.hpp"
 
 namespace samhip {
@@ -24,7 +35,7 @@ constexpr int kQkvThreads = kQkvTok * kQkvLanes;
 template <typename T, int VE>  // VE elements per vector access (16 bytes, or 1 when hd is odd-sized)
 __global__ __launch_bounds__(kQkvThreads) void qkv_split_kernel(const T* __restrict__ y, const T* __restrict__ bias,
                                                                T* __restrict__ out, int n, int nh, int hd, int tiles,
-                                                               int tt, long plane) {
+                                                               int tt, long plane, int gh, int gw, int ws) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* kt_tile = reinterpret_cast<float*>(smem);  // [hd][kQkvTok + 1]
   typedef typename Vec<T>::x8 V8;
@@ -41,9 +52,17 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_split_kernel(const T* __restr
   const long bh = win * nh + head;
   const int vpr = hd / VE;  // vectors per token row of one head
   const int tok = threadIdx.x / kQkvLanes, lane = threadIdx.x % kQkvLanes;
+  // the token's row of y: window order, or its place on the grid (-1: a padding token)
+  long t = win * n + n0 + tok;
+  if (gw > 0) {
+    const int nww = (gw + ws - 1) / ws, nwin = ((gh + ws - 1) / ws) * nww;
+    const long wb = win / nwin;
+    const int wr = (int)(win - wb * nwin), wi = wr / nww, wj = wr - wi * nww;
+    const int i = n0 + tok, ti = i / ws, tj = i - ti * ws, r = wi * ws + ti, c = wj * ws + tj;
+    t = r < gh && c < gw ? (wb * gh + r) * gw + c : -1;
+  }
   if (tok < ntok) {
-    const long t = win * n + n0 + tok;
-    const T* yrow = y + t * 3L * C + head * hd;
+    const T* yrow = y + (t < 0 ? 0 : t) * 3L * C + head * hd;
 #pragma unroll
     for (int which = 0; which < 3; ++which) {
       const T* src = yrow + which * C;
@@ -53,12 +72,12 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_split_kernel(const T* __restr
         const int d0 = v * VE;
         float vals[VE];
         if constexpr (VE == 8) {
-          const V8 a = *reinterpret_cast<const V8*>(src + d0);
+          const V8 a = t < 0 ? V8{} : *reinterpret_cast<const V8*>(src + d0);
           const V8 bb = *reinterpret_cast<const V8*>(bsrc + d0);
 #pragma unroll
           for (int e = 0; e < 8; ++e) vals[e] = to_f32(a[e]) + to_f32(bb[e]);
         } else {
-          vals[0] = to_f32(src[d0]) + to_f32(bsrc[d0]);
+          vals[0] = (t < 0 ? 0.f : to_f32(src[d0])) + to_f32(bsrc[d0]);
         }
         if (which == 1) {
 #pragma unroll
@@ -85,7 +104,7 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_split_kernel(const T* __restr
 
 template <typename T>
 static hipError_t launch_qkv(const void* y, const void* bias, void* out, long tokens, int n, int nh, int hd,
-                             hipStream_t stream) {
+                             hipStream_t stream, int gh = 0, int gw = 0, int ws = 0) {
   const long windows = tokens / n;
   const int tiles = (n + kQkvTok - 1) / kQkvTok;
   const int tt = (n + tiles - 1) / tiles;  // balanced tiles of at most kQkvTok tokens
@@ -94,10 +113,10 @@ static hipError_t launch_qkv(const void* y, const void* bias, void* out, long to
   const size_t lds = (size_t)hd * (kQkvTok + 1) * sizeof(float);
   if (hd % 8 == 0)
     hipLaunchKernelGGL((qkv_split_kernel<T, 8>), dim3((unsigned)blocks), dim3(kQkvThreads), lds, stream,
-                       (const T*)y, (const T*)bias, (T*)out, n, nh, hd, tiles, tt, plane);
+                       (const T*)y, (const T*)bias, (T*)out, n, nh, hd, tiles, tt, plane, gh, gw, ws);
   else
     hipLaunchKernelGGL((qkv_split_kernel<T, 1>), dim3((unsigned)blocks), dim3(kQkvThreads), lds, stream,
-                       (const T*)y, (const T*)bias, (T*)out, n, nh, hd, tiles, tt, plane);
+                       (const T*)y, (const T*)bias, (T*)out, n, nh, hd, tiles, tt, plane, gh, gw, ws);
   return hipGetLastError();
 }
 
@@ -107,6 +126,64 @@ hipError_t qkv_split(int dtype, const void* y, const void* bias, void* out, long
   if (dtype == kF32) return launch_qkv<float>(y, bias, out, tokens, n, nh, hd, stream);
   if (dtype == kF16) return launch_qkv<f16>(y, bias, out, tokens, n, nh, hd, stream);
   return launch_qkv<bf16>(y, bias, out, tokens, n, nh, hd, stream);
+}
+
+// Checked by the caller: batch, gh, gw, ws, nh >= 1, hd <= 256; tokens = windows * ws * ws with the
+// padded grid's windows; the sizes fit as in qkv_split.
+hipError_t qkv_split_grid(int dtype, const void* y, const void* bias, void* out, int batch, int gh, int gw, int ws,
+                          int nh, int hd, hipStream_t stream) {
+  const long tokens = (long)batch * ((gh + ws - 1) / ws) * ((gw + ws - 1) / ws) * ws * ws;
+  const int n = ws * ws;
+  if (dtype == kF32) return launch_qkv<float>(y, bias, out, tokens, n, nh, hd, stream, gh, gw, ws);
+  if (dtype == kF16) return launch_qkv<f16>(y, bias, out, tokens, n, nh, hd, stream, gh, gw, ws);
+  return launch_qkv<bf16>(y, bias, out, tokens, n, nh, hd, stream, gh, gw, ws);
+}
+
+template <typename T, int VE>
+__global__ __launch_bounds__(256) void window_merge_kernel(const T* __restrict__ ctx, T* __restrict__ out, int gh,
+                                                          int gw, int ws, int nh, int hd, long nvec) {
+  typedef T TV __attribute__((ext_vector_type(VE)));
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nvec) return;
+  const int C = nh * hd;
+  const long e = i * VE;                   // output element: ((b*gh + r)*gw + c)*C + h*hd + d
+  const long tokc = e / C;
+  const int col = (int)(e - tokc * C), h = col / hd, d = col - h * hd;
+  const long bg = tokc / gw;
+  const int c = (int)(tokc - bg * gw);
+  const long b = bg / gh;
+  const int r = (int)(bg - b * gh);
+  const int nww = (gw + ws - 1) / ws, nwh = (gh + ws - 1) / ws;
+  const long win = (b * nwh + r / ws) * nww + c / ws;
+  const int tok = (r % ws) * ws + c % ws;
+  *reinterpret_cast<TV*>(out + e) = *reinterpret_cast<const TV*>(ctx + ((win * nh + h) * ws * ws + tok) * hd + d);
+}
+
+template <typename T>
+static hipError_t launch_merge(const void* ctx, void* out, int batch, int gh, int gw, int ws, int nh, int hd,
+                               hipStream_t stream) {
+  const long elems = (long)batch * gh * gw * nh * hd;
+  const int ve = hd % (16 / (int)sizeof(T)) == 0 ? 16 / (int)sizeof(T) : (hd % 2 == 0 ? 2 : 1);
+  const long nvec = elems / ve;
+  const unsigned blocks = (unsigned)((nvec + 255) / 256);
+  if (ve == 16 / (int)sizeof(T))
+    hipLaunchKernelGGL((window_merge_kernel<T, 16 / sizeof(T)>), dim3(blocks), dim3(256), 0, stream, (const T*)ctx,
+                       (T*)out, gh, gw, ws, nh, hd, nvec);
+  else if (ve == 2)
+    hipLaunchKernelGGL((window_merge_kernel<T, 2>), dim3(blocks), dim3(256), 0, stream, (const T*)ctx, (T*)out, gh,
+                       gw, ws, nh, hd, nvec);
+  else
+    hipLaunchKernelGGL((window_merge_kernel<T, 1>), dim3(blocks), dim3(256), 0, stream, (const T*)ctx, (T*)out, gh,
+                       gw, ws, nh, hd, nvec);
+  return hipGetLastError();
+}
+
+// Checked by the caller: batch, gh, gw, ws, nh, hd >= 1, 16-byte aligned pointers, sizes below 2^40.
+hipError_t window_merge(int dtype, const void* ctx, void* out, int batch, int gh, int gw, int ws, int nh, int hd,
+                        hipStream_t stream) {
+  if (dtype == kF32) return launch_merge<float>(ctx, out, batch, gh, gw, ws, nh, hd, stream);
+  if (dtype == kF16) return launch_merge<f16>(ctx, out, batch, gh, gw, ws, nh, hd, stream);
+  return launch_merge<bf16>(ctx, out, batch, gh, gw, ws, nh, hd, stream);
 }
 
 }  // namespace samhip

@@ -24,6 +24,10 @@ hipError_t relpos_softmax(int dtype, const void* s, const void* q, const void* t
                           int hd, float scale, hipStream_t stream);
 hipError_t qkv_split(int dtype, const void* y, const void* bias, void* out, long tokens, int n, int nh, int hd,
                      hipStream_t stream);
+hipError_t qkv_split_grid(int dtype, const void* y, const void* bias, void* out, int batch, int gh, int gw, int ws,
+                          int nh, int hd, hipStream_t stream);
+hipError_t window_merge(int dtype, const void* ctx, void* out, int batch, int gh, int gw, int ws, int nh, int hd,
+                        hipStream_t stream);
 hipError_t preprocess(int dtype, const void* img, void* out, int h, int w, int nh, int nw, int size, const float* mean,
                       const float* stdv, hipStream_t stream);
 int preprocess_max_taps(int n, int nout);
@@ -223,6 +227,44 @@ int sam_hip_qkv_split(const void* y, const void* bias, void* out, int dtype, lon
     return fail(SAM_HIP_EUNSUPPORTED, "qkv-split: y, bias and out must be 16-byte aligned");
   hipError_t e = samhip::qkv_split(dtype, y, bias, out, tokens, n, nh, hd, reinterpret_cast<hipStream_t>(stream));
   return check_launch(e, "qkv-split");
+}
+
+int sam_hip_qkv_split_grid(const void* y, const void* bias, void* out, int dtype, int batch, int gh, int gw, int ws,
+                           int nh, int hd, void* stream) {
+  if (!y || !bias || !out) return fail(SAM_HIP_EINVAL, "qkv-split-grid: null pointer argument");
+  if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
+  if (batch <= 0 || gh <= 0 || gw <= 0 || ws <= 0 || nh <= 0 || hd <= 0)
+    return fail(SAM_HIP_EINVAL, "qkv-split-grid: sizes must be positive (batch=%d gh=%d gw=%d ws=%d nh=%d hd=%d)",
+                batch, gh, gw, ws, nh, hd);
+  if (hd > 256) return fail(SAM_HIP_EUNSUPPORTED, "qkv-split-grid: head dim at most 256, got %d", hd);
+  if (gh > 4096 || gw > 4096 || ws > 256) return fail(SAM_HIP_EUNSUPPORTED, "qkv-split-grid: grid or window too large");
+  const long windows = (long)batch * ((gh + ws - 1) / ws) * ((gw + ws - 1) / ws);
+  const long n = (long)ws * ws;
+  if (windows * ((n + 63) / 64) * nh > 0x7fffffffL || windows * n * 3L * nh * hd >= (1L << 40))
+    return fail(SAM_HIP_EUNSUPPORTED, "qkv-split-grid: too many tokens");
+  if (!aligned16(y) || !aligned16(bias) || !aligned16(out))
+    return fail(SAM_HIP_EUNSUPPORTED, "qkv-split-grid: y, bias and out must be 16-byte aligned");
+  hipError_t e =
+      samhip::qkv_split_grid(dtype, y, bias, out, batch, gh, gw, ws, nh, hd, reinterpret_cast<hipStream_t>(stream));
+  return check_launch(e, "qkv-split-grid");
+}
+
+int sam_hip_window_merge(const void* ctx, void* out, int dtype, int batch, int gh, int gw, int ws, int nh, int hd,
+                         void* stream) {
+  if (!ctx || !out) return fail(SAM_HIP_EINVAL, "window-merge: null pointer argument");
+  if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
+  if (batch <= 0 || gh <= 0 || gw <= 0 || ws <= 0 || nh <= 0 || hd <= 0)
+    return fail(SAM_HIP_EINVAL, "window-merge: sizes must be positive (batch=%d gh=%d gw=%d ws=%d nh=%d hd=%d)", batch,
+                gh, gw, ws, nh, hd);
+  if (gh > 4096 || gw > 4096 || ws > 256 || hd > 4096)
+    return fail(SAM_HIP_EUNSUPPORTED, "window-merge: grid, window or head dim too large");
+  const long windows = (long)batch * ((gh + ws - 1) / ws) * ((gw + ws - 1) / ws);
+  if (windows * ws * ws * (long)nh * hd >= (1L << 38))
+    return fail(SAM_HIP_EUNSUPPORTED, "window-merge: too many elements");
+  if (!aligned16(ctx) || !aligned16(out))
+    return fail(SAM_HIP_EUNSUPPORTED, "window-merge: ctx and out must be 16-byte aligned");
+  hipError_t e = samhip::window_merge(dtype, ctx, out, batch, gh, gw, ws, nh, hd, reinterpret_cast<hipStream_t>(stream));
+  return check_launch(e, "window-merge");
 }
 
 }  // extern "C"

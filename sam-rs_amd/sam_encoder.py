@@ -3,16 +3,19 @@
 Mirrors sam1::encoder::ImageEncoder (sam1/encoder.rs:1-200): patch embedding, absolute position
 embedding, `depth` blocks (windowed 14x14 or global attention with decomposed rel-pos, MLP with exact
 GELU) and the neck. Per block, the reference's kernel calls map to:
-- qkv_split (kernels.rs:872) -> sam_hip.qkv_split;
+- window_partition + qkv_split (encoder.rs:129-137, kernels.rs:872) -> sam_hip.qkv_split_grid;
 - attention_relpos / relpos_softmax + bmm (encoder.rs:79-82) -> sam_hip.attention_relpos (fused);
+- the head merge and window_unpartition (encoder.rs:83, 140-143) -> sam_hip.window_merge;
 - bias_residual (kernels.rs:1040) -> sam_hip.bias_residual;
 - bias_gelu (kernels.rs:1052) -> sam_hip.bias_gelu.
 
 The linears run as torch matmuls (hipBLASLt) and LayerNorm as torch's layer_norm. The two
 convolutions are exact GEMMs: the 16x16 stride-16 patch embedding over non-overlapping patches, and
-the neck's 3x3 conv as an unfold. Window partition zero-pads the token grid to a multiple of the
-window (encoder.rs:134-138): the padded tokens are real keys with no mask, whose q/k/v equal the qkv
-bias, as in the reference.
+the neck's 3x3 conv as an unfold. The reference's window partition zero-pads the token grid to a
+multiple of the window (encoder.rs:134-138): the padded tokens are real keys with no mask, whose
+q/k/v equal the qkv bias. The linears act on each token alone, so here they run on the grid's tokens
+and qkv_split_grid writes the padded windows' q/k/v (the bias for padding tokens), which is the
+same. window_partition / window_unpartition below are the reference's steps, kept for the tests.
 """
 from __future__ import annotations
 
@@ -122,25 +125,31 @@ def window_unpartition(x: torch.Tensor, ws: int, hp: int, wp: int, hw, b: int, c
 
 
 def attention(x: torch.Tensor, p: BlockWeights, heads: int) -> torch.Tensor:
-    """encoder.rs:73-85: [nW, h, w, C] -> the output projection without its bias, [nW, h, w, C]."""
-    nw, h, w, c = x.shape
-    n, hd = h * w, c // heads
-    y = x.reshape(nw * n, c) @ p.qkv_wt
-    q, kt, v = sam_hip.qkv_split(y, p.qkv_b, n, heads, hd)
-    ctx = sam_hip.attention_relpos(q, kt, v, p.rel, h, w, hd ** -0.5)
-    out = ctx.view(nw, heads, n, hd).permute(0, 2, 1, 3).reshape(nw * n, c)
-    return (out @ p.proj_wt).view(nw, h, w, c)
+    """encoder.rs:73-85 with the window partition and unpartition of encoder.rs:129-143 around it:
+    [B, H, W, C] -> the output projection without its bias, [B, H, W, C].
+
+    The qkv and proj linears act on each token alone, so they run on the H*W grid tokens instead of
+    the zero-padded windows: sam_hip.qkv_split_grid cuts the windows from the grid's projection (a
+    padding token's q, k and v are the bias alone, as the padded zeros give), and
+    sam_hip.window_merge puts the attention output back on the grid with the heads merged. A global
+    block is one window of the whole grid."""
+    b, h, w, c = x.shape
+    ws = p.window if p.window > 0 else h
+    wsw = p.window if p.window > 0 else w
+    if ws != wsw:
+        raise ValueError("square windows only")
+    hd = c // heads
+    y = x.reshape(b * h * w, c) @ p.qkv_wt
+    q, kt, v = sam_hip.qkv_split_grid(y, p.qkv_b, b, h, w, ws, heads, hd)
+    ctx = sam_hip.attention_relpos(q, kt, v, p.rel, ws, ws, hd ** -0.5)
+    out = sam_hip.window_merge(ctx, b, h, w, ws, heads).reshape(b * h * w, c)
+    return (out @ p.proj_wt).view(b, h, w, c)
 
 
 def block(x: torch.Tensor, p: BlockWeights, heads: int) -> torch.Tensor:
     """encoder.rs:112-126."""
     b, h, w, c = x.shape
-    y = F.layer_norm(x, (c,), p.norm1_w, p.norm1_b, 1e-6)
-    if p.window > 0:
-        parts, hp, wp = window_partition(y, p.window)
-        y = window_unpartition(attention(parts, p, heads), p.window, hp, wp, (h, w), b, c)
-    else:
-        y = attention(y, p, heads)
+    y = attention(F.layer_norm(x, (c,), p.norm1_w, p.norm1_b, 1e-6), p, heads)
     x = sam_hip.bias_residual(x, y, p.proj_b)
     t = b * h * w
     m = sam_hip.bias_gelu(F.layer_norm(x, (c,), p.norm2_w, p.norm2_b, 1e-6).reshape(t, c) @ p.lin1_wt, p.lin1_b)

@@ -63,6 +63,10 @@ def load():
         L.sam_hip_relpos_softmax.restype = _i
         L.sam_hip_qkv_split.argtypes = [_vp] * 3 + [_i, ctypes.c_long, _i, _i, _i, _vp]
         L.sam_hip_qkv_split.restype = _i
+        L.sam_hip_qkv_split_grid.argtypes = [_vp] * 3 + [_i] * 7 + [_vp]
+        L.sam_hip_qkv_split_grid.restype = _i
+        L.sam_hip_window_merge.argtypes = [_vp] * 2 + [_i] * 7 + [_vp]
+        L.sam_hip_window_merge.restype = _i
         _lp = ctypes.POINTER(ctypes.c_long)
         L.sam_hip_flash_attn_workspace_size.argtypes = [_i] * 7
         L.sam_hip_flash_attn_workspace_size.restype = ctypes.c_long
@@ -291,6 +295,38 @@ def qkv_split(y: torch.Tensor, bias: torch.Tensor, n: int, nh: int, hd: int):
     packed = torch.empty((3, t * nh * hd), dtype=y.dtype, device=y.device)
     _check(load().sam_hip_qkv_split(y.data_ptr(), bias.data_ptr(), packed.data_ptr(), dt, t, n, nh, hd, _stream()))
     return packed[0].view(bh, n, hd), packed[1].view(bh, hd, n), packed[2].view(bh, n, hd)
+
+
+def qkv_split_grid(y: torch.Tensor, bias: torch.Tensor, batch: int, gh: int, gw: int, ws: int, nh: int, hd: int):
+    """y: [batch*gh*gw, 3*nh*hd] (bias-free qkv projection of the unpadded grid tokens) + bias ->
+    (q [BH, ws*ws, hd], kT [BH, hd, ws*ws], v [BH, ws*ws, hd]) for the windows of the grid zero-padded to
+    multiples of ws (padding tokens: the bias alone), BH = batch * ceil(gh/ws) * ceil(gw/ws) * nh."""
+    y = y.contiguous()
+    _contig(y, bias)
+    dt = _dtype(y, bias)
+    if y.shape != (batch * gh * gw, 3 * nh * hd) or bias.shape != (3 * nh * hd,):
+        raise SamHipError(f"qkv_split_grid: y must be [{batch * gh * gw}, {3 * nh * hd}] and bias [{3 * nh * hd}], "
+                          f"got {tuple(y.shape)} and {tuple(bias.shape)}")
+    n = ws * ws
+    bh = batch * (-(-gh // ws)) * (-(-gw // ws)) * nh
+    packed = torch.empty((3, bh * n * hd), dtype=y.dtype, device=y.device)
+    _check(load().sam_hip_qkv_split_grid(y.data_ptr(), bias.data_ptr(), packed.data_ptr(), dt, batch, gh, gw, ws, nh,
+                                         hd, _stream()))
+    return packed[0].view(bh, n, hd), packed[1].view(bh, hd, n), packed[2].view(bh, n, hd)
+
+
+def window_merge(ctx: torch.Tensor, batch: int, gh: int, gw: int, ws: int, nh: int) -> torch.Tensor:
+    """ctx [BH, ws*ws, hd] in qkv_split_grid's window order -> [batch, gh, gw, nh*hd] (heads merged,
+    windows back on the grid without their padding)."""
+    ctx = ctx.contiguous()
+    _contig(ctx)
+    dt = _dtype(ctx)
+    bh, n, hd = ctx.shape
+    if n != ws * ws or bh != batch * (-(-gh // ws)) * (-(-gw // ws)) * nh:
+        raise SamHipError(f"window_merge: ctx {tuple(ctx.shape)} does not hold the windows of a {gh}x{gw} grid")
+    out = torch.empty((batch, gh, gw, nh * hd), dtype=ctx.dtype, device=ctx.device)
+    _check(load().sam_hip_window_merge(ctx.data_ptr(), out.data_ptr(), dt, batch, gh, gw, ws, nh, hd, _stream()))
+    return out
 
 
 def _strides_blhd(t: torch.Tensor, layout: str):

@@ -28,7 +28,7 @@ def test_header_declares_the_entry_points():
     names = declared_functions()
     for want in ("sam_hip_attn_relpos", "sam_hip_relpos_softmax", "sam_hip_qkv_split", "sam_hip_deform_attn",
                  "sam_hip_flash_attn", "sam_hip_flash_attn_workspace_size", "sam_hip_flash_attn_noalloc", "sam_hip_rope", "sam_hip_last_error",
-                 "sam_hip_abi_version"):
+                 "sam_hip_abi_version", "sam_hip_qkv_split_grid", "sam_hip_window_merge"):
         assert want in names
 
 
@@ -55,6 +55,16 @@ def test_null_pointers_and_bad_sizes_fail_without_a_launch(lib):
     assert lib.sam_hip_deform_attn(fake, fake, fake, fake, 0, 1, 31, 3, 2, 8, 2, 2, shapes, None) == 1
     lib.sam_hip_qkv_split.argtypes = [vp] * 3 + [i, ctypes.c_long, i, i, i, vp]
     assert lib.sam_hip_qkv_split(fake, fake, fake, 1, 100, 7, 2, 8, None) == 1  # 100 % 7 != 0
+    lib.sam_hip_qkv_split_grid.argtypes = [vp] * 3 + [i] * 7 + [vp]
+    assert lib.sam_hip_qkv_split_grid(None, fake, fake, 1, 1, 64, 64, 14, 16, 80, None) == 1
+    assert lib.sam_hip_qkv_split_grid(fake, fake, fake, 1, 1, 64, 0, 14, 16, 80, None) == 1
+    assert lib.sam_hip_qkv_split_grid(fake, fake, fake, 1, 1, 64, 64, 14, 16, 264, None) == 3
+    assert lib.sam_hip_qkv_split_grid(fake, fake, fake, 5, 1, 64, 64, 14, 16, 80, None) == 2
+    lib.sam_hip_window_merge.argtypes = [vp] * 2 + [i] * 7 + [vp]
+    assert lib.sam_hip_window_merge(fake, None, 1, 1, 64, 64, 14, 16, 80, None) == 1
+    assert lib.sam_hip_window_merge(fake, fake, 1, 1, 64, 64, 0, 16, 80, None) == 1
+    assert lib.sam_hip_window_merge(fake, fake, 1, 1, 64, 64, 300, 16, 80, None) == 3
+    assert lib.sam_hip_window_merge(vp(0x1004), fake, 1, 1, 64, 64, 14, 16, 80, None) == 3  # misaligned
 
 
 def test_flash_and_rope_argument_checks(lib):

@@ -128,3 +128,54 @@ def test_qkv_split_is_bit_exact(hip, n, nh, hd, win, dtype):
     for a, want in ((q1, q0), (k1, k0), (v1, v0)):
         assert tuple(a.shape) == want.shape
         assert np.array_equal(a.float().cpu().numpy(), want)
+
+
+def partition_np(y, batch, gh, gw, ws):
+    """The reference's window partition (sam1/encoder.rs:129-137) of grid rows [batch*gh*gw, c]: zero
+    padding to multiples of ws, windows (b, wi, wj) in order, tokens (ti, tj) row-major."""
+    c = y.shape[1]
+    ph, pw = -gh % ws, -gw % ws
+    g = np.pad(y.reshape(batch, gh, gw, c), ((0, 0), (0, ph), (0, pw), (0, 0)))
+    hp, wp = gh + ph, gw + pw
+    return g.reshape(batch, hp // ws, ws, wp // ws, ws, c).transpose(0, 1, 3, 2, 4, 5).reshape(-1, c)
+
+
+# (batch, gh, gw, ws, nh, hd): the ViT-H windowed block (64x64 grid, 14x14 windows, 16 heads x 80), a
+# grid already a multiple of the window, one with padding on both sides and odd head dims, the global
+# block as one 64x64 window, and a window larger than the grid
+GRID_SHAPES = [(1, 64, 64, 14, 16, 80), (2, 28, 28, 14, 2, 64), (2, 20, 13, 7, 3, 12), (1, 64, 64, 64, 2, 80),
+               (1, 5, 6, 8, 1, 16)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("batch,gh,gw,ws,nh,hd", GRID_SHAPES)
+def test_qkv_split_grid_equals_partition_then_split(hip, batch, gh, gw, ws, nh, hd, dtype):
+    """qkv_split_grid on the grid's projection = qkv_split on the projection of the zero-padded windows
+    (whose padding rows are 0), bit for bit."""
+    print(f"qkv_split_grid {dtype} batch={batch} grid={gh}x{gw} ws={ws} nh={nh} hd={hd}", flush=True)
+    r = np.random.default_rng(gh * 31 + gw + hd)
+    y = oracle.round_to(r.standard_normal((batch * gh * gw, 3 * nh * hd)), dtype)
+    b = oracle.round_to(r.standard_normal(3 * nh * hd), dtype)
+    q0, k0, v0 = (oracle.round_to(x, dtype) for x in oracle.qkv_split(partition_np(y, batch, gh, gw, ws), b, ws * ws,
+                                                                         nh, hd))
+    q1, k1, v1 = hip.qkv_split_grid(dev(y, dtype), dev(b, dtype), batch, gh, gw, ws, nh, hd)
+    for a, want in ((q1, q0), (k1, k0), (v1, v0)):
+        assert tuple(a.shape) == want.shape
+        assert np.array_equal(a.float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("batch,gh,gw,ws,nh,hd", GRID_SHAPES)
+def test_window_merge_is_unpartition_of_merged_heads(hip, batch, gh, gw, ws, nh, hd, dtype):
+    """window_merge(ctx) = window_unpartition (sam1/encoder.rs:140-143) of the heads merged as
+    sam1/encoder.rs:83 merges them, cropped to the grid: a copy, bit for bit."""
+    print(f"window_merge {dtype} batch={batch} grid={gh}x{gw} ws={ws} nh={nh} hd={hd}", flush=True)
+    nwh, nww = -(-gh // ws), -(-gw // ws)
+    bh, n = batch * nwh * nww * nh, ws * ws
+    r = np.random.default_rng(gh * 7 + gw + hd)
+    ctx = oracle.round_to(r.standard_normal((bh, n, hd)), dtype)
+    merged = ctx.reshape(batch * nwh * nww, nh, n, hd).transpose(0, 2, 1, 3).reshape(batch, nwh, nww, ws, ws, nh * hd)
+    want = merged.transpose(0, 1, 3, 2, 4, 5).reshape(batch, nwh * ws, nww * ws, nh * hd)[:, :gh, :gw]
+    got = hip.window_merge(dev(ctx, dtype), batch, gh, gw, ws, nh).float().cpu().numpy()
+    assert got.shape == want.shape
+    assert np.array_equal(got, want)
