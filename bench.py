@@ -157,15 +157,23 @@ def traffic_from_profiles():
 
 class Timer:
     """One pair of HIP events on the launch stream around reps back-to-back calls; the average call
-    time in ms (no markers between the calls)."""
+    time in ms (no markers between the calls).
+
+    Before timing, fn runs at least `warmup` times and for at least `warm_s` seconds of GPU time: the
+    chip reaches its steady clock only after tens of milliseconds of load, and a leg timed right after
+    host-side work (the CPU baselines) would otherwise run its few timed calls on the ramp."""
 
     def __init__(self, torch, stream):
         self.torch, self.stream = torch, stream
 
-    def avg_ms(self, fn, reps, warmup=2):
-        for _ in range(warmup):
-            fn()
-        self.torch.cuda.synchronize()
+    def avg_ms(self, fn, reps, warmup=2, warm_s=0.05):
+        t0 = time.perf_counter()
+        n = 0
+        while n < warmup or time.perf_counter() - t0 < warm_s:
+            for _ in range(max(warmup, 1)):
+                fn()
+            n += max(warmup, 1)
+            self.torch.cuda.synchronize()
         a, b = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
         a.record(self.stream)
         for _ in range(reps):
@@ -389,7 +397,7 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
                                         "best of 3")
 
     # The encoder attention sweep (ViT-B / ViT-L / ViT-H, f16, batch 1, 4 and 8): every attention layer of
-    # the encoder on fresh q/kT/v per layer, back to back, in ms per image. Windowed layers are
+    # the encoder, each layer on its own q/kT/v, back to back, in ms per image. Windowed layers are
     # batch x 25 windows x heads units of 14x14; global layers batch x heads 64x64 grids.
     for mname, (depth, heads, hd, glob) in (("vit_b", (12, 12, 64, (2, 5, 8, 11))),
                                             ("vit_l", (24, 16, 64, (5, 11, 17, 23))),
@@ -407,13 +415,19 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
                 v = torch.randn(bh, n, hd, device=dev, generator=g).half()
                 table = (0.02 * torch.randn(4 * side - 2, hd, device=dev, generator=g)).half()
                 out = torch.empty_like(q)
+                # one input set per layer, as in the encoder: a repeated set would stay in the 256 MB
+                # last-level cache (a ViT-H windowed layer at batch 1 reads 50 MB)
+                sets = [(q, kt, v, out)] + [(q.clone(), kt.clone(), v.clone(), torch.empty_like(q))
+                                            for _ in range(count - 1)]
 
                 def run():
-                    check(lib, lib.sam_hip_attn_relpos(q.data_ptr(), kt.data_ptr(), v.data_ptr(), table.data_ptr(),
-                                                       out.data_ptr(), 1, bh, side, side, hd, hd ** -0.5, sp))
+                    for qq, kk, vv, oo in sets:
+                        check(lib, lib.sam_hip_attn_relpos(qq.data_ptr(), kk.data_ptr(), vv.data_ptr(),
+                                                           table.data_ptr(), oo.data_ptr(), 1, bh, side, side, hd,
+                                                           hd ** -0.5, sp))
 
-                layer_us[side] = (timer.avg_ms(run, 10 if batch > 1 else 30) * 1e3, count, bh, n)
-                del q, kt, v, out
+                layer_us[side] = (timer.avg_ms(run, 10 if batch > 1 else 30) * 1e3 / len(sets), count, bh, n)
+                del q, kt, v, out, sets
             total_ms = sum(us * c for us, c, _, _ in layer_us.values()) / 1e3
             gf = sum(flops(bh, n, hd) * c for _, c, bh, n in layer_us.values()) / 1e9
             res[f"sweep_{mname}_attention_b{batch}_f16"] = {
