@@ -31,7 +31,7 @@ def ref_attention(x, p, heads):
     without its bias."""
     nw, h, w, c = x.shape
     hd, n = c // heads, h * w
-    qkv = (x.reshape(nw, n, c) @ p.qkv_wt.float() + p.qkv_b.float()).view(nw, n, 3, heads, hd)
+    qkv = (x.reshape(nw, n, c) @ p.qkv_w.float().t() + p.qkv_b.float()).view(nw, n, 3, heads, hd)
     q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3).contiguous() for i in range(3))  # [nw, heads, n, hd]
     rel = p.rel.float()
     rel_h, rel_w = rel[: 2 * h - 1], rel[2 * h - 1:]
@@ -46,13 +46,13 @@ def ref_attention(x, p, heads):
     s = s.view(nw, heads, h, w, h, w) + bias_h[..., :, None] + bias_w[..., None, :]
     a = torch.softmax(s.view(nw, heads, n, n), -1)
     o = (a @ v).permute(0, 2, 1, 3).reshape(nw, n, c)
-    return (o @ p.proj_wt.float()).view(nw, h, w, c)
+    return (o @ p.proj_w.float().t()).view(nw, h, w, c)
 
 
 def ref_forward(img, w, enc):
     cfg = w.cfg
     c, k, o = cfg.embed_dim, cfg.patch, cfg.out_chans
-    wconv = w.patch_wt.float().t().reshape(c, 3, k, k)
+    wconv = w.patch_w.float().reshape(c, 3, k, k)
     # convolutions on the CPU: torch's own conv2d, independent of the GEMM forms the encoder uses
     x = F.conv2d(img.float().cpu(), wconv.cpu(), w.patch_b.float().cpu(), stride=k).cuda()
     x = x.permute(0, 2, 3, 1) + w.pos.float()
@@ -65,12 +65,13 @@ def ref_forward(img, w, enc):
         else:
             y = ref_attention(y, p, cfg.heads)
         x = x + y + p.proj_b.float()
-        m = F.layer_norm(x, (c,), p.norm2_w.float(), p.norm2_b.float(), 1e-6) @ p.lin1_wt.float() + p.lin1_b.float()
-        x = x + F.gelu(m) @ p.lin2_wt.float() + p.lin2_b.float()
+        m = F.layer_norm(x, (c,), p.norm2_w.float(), p.norm2_b.float(), 1e-6)
+        m = m @ p.lin1_w.float().t() + p.lin1_b.float()
+        x = x + F.gelu(m) @ p.lin2_w.float().t() + p.lin2_b.float()
     x = x.permute(0, 3, 1, 2)
-    y = F.conv2d(x.cpu(), w.neck0_wt.float().t().reshape(o, c, 1, 1).cpu()).cuda()
+    y = F.conv2d(x.cpu(), w.neck0_w.float().reshape(o, c, 1, 1).cpu()).cuda()
     y = F.layer_norm(y.permute(0, 2, 3, 1), (o,), w.neck1_w.float(), w.neck1_b.float(), 1e-6).permute(0, 3, 1, 2)
-    y = F.conv2d(y.cpu(), w.neck2_wt.float().t().reshape(o, o, 3, 3).cpu(), padding=1).cuda()
+    y = F.conv2d(y.cpu(), w.neck2_w.float().reshape(o, o, 3, 3).cpu(), padding=1).cuda()
     return F.layer_norm(y.permute(0, 2, 3, 1), (o,), w.neck3_w.float(), w.neck3_b.float(), 1e-6).permute(0, 3, 1, 2)
 
 
