@@ -183,6 +183,29 @@ class Timer:
         return a.elapsed_time(b) / reps
 
 
+LLC_SPAN = 768 << 20  # three times MI355X's 256 MB last-level cache
+
+
+def cold_sets(nbytes, *tensors):
+    """Copies of a leg's operands (inputs and outputs) to cycle through: enough that more than the
+    last-level cache is touched between two uses of one copy, so that an HBM-bound leg reads its
+    operands from HBM on every timed call, as a model step does, and not from the cache that a
+    repeated call on one set leaves them in."""
+    n = max(1, -(-LLC_SPAN // int(nbytes)))
+    return [tensors] + [tuple(t.clone() for t in tensors) for _ in range(n - 1)]
+
+
+class Cycle:
+    """A leg's timed call: fn on the next operand set each time."""
+
+    def __init__(self, sets, fn):
+        self.sets, self.fn, self.i = sets, fn, 0
+
+    def __call__(self):
+        self.fn(*self.sets[self.i])
+        self.i = (self.i + 1) % len(self.sets)
+
+
 def check(lib, rc):
     if rc:
         raise RuntimeError(lib.sam_hip_last_error().decode())
@@ -282,13 +305,13 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
         attn_w = torch.softmax(torch.randn(1, q, hh, ll * pp, device=dev, generator=g), -1).view(1, q, hh, ll, pp)
         attn_w = attn_w.contiguous()
         out = torch.empty(1, q, hh * dd, device=dev)
-
-        def run():
-            check(lib, lib.sam_hip_deform_attn(value.data_ptr(), loc.data_ptr(), attn_w.data_ptr(), out.data_ptr(), 0,
-                                               1, s, q, hh, dd, ll, pp, flat, sp))
-
-        ms = timer.avg_ms(run, 50)
         nbytes = 4.0 * (s * hh * dd + 3 * q * hh * ll * pp + q * hh * dd)
+        run = Cycle(cold_sets(nbytes, value, loc, attn_w, out),
+                    lambda va, lo, aw, o: check(lib, lib.sam_hip_deform_attn(va.data_ptr(), lo.data_ptr(), aw.data_ptr(),
+                                                                             o.data_ptr(), 0, 1, s, q, hh, dd, ll, pp,
+                                                                             flat, sp)))
+        ms = timer.avg_ms(run, 50)
+        del run
         gathered = 4.0 * q * hh * ll * pp * 4 * dd
         res[f"dino_deform_{name}_f32"] = {
             "workload": f"Grounding DINO-tiny deformable attention, {q} queries over {s} values, 8 heads x 32, "
@@ -312,12 +335,14 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
                           -1).expand(1, q, ll, 4)).contiguous()
         logits = torch.randn(1, q, hh, ll, pp, device=dev, generator=g)
 
-        def run_core():
-            check(lib, lib.sam_hip_deform_core(value.data_ptr(), off.data_ptr(), logits.data_ptr(), refs.data_ptr(),
-                                               out.data_ptr(), 0, 1, s, q, hh, dd, ll, pp, refs.shape[3], flat, sp))
-
-        ms = timer.avg_ms(run_core, 50)
         nbytes = 4.0 * (s * hh * dd + 3 * q * hh * ll * pp + q * ll * refs.shape[3] + q * hh * dd)
+        nref = refs.shape[3]
+        run_core = Cycle(cold_sets(nbytes, value, off, logits, refs, out),
+                         lambda va, of, lg, rf, o: check(lib, lib.sam_hip_deform_core(
+                             va.data_ptr(), of.data_ptr(), lg.data_ptr(), rf.data_ptr(), o.data_ptr(), 0, 1, s, q, hh,
+                             dd, ll, pp, nref, flat, sp)))
+        ms = timer.avg_ms(run_core, 50)
+        del run_core
         res[f"dino_deform_core_{name}_f32"] = {
             "workload": f"Grounding DINO-tiny Deform::forward core (logit softmax + {refs.shape[3]}-coordinate "
                         f"sampling locations + gather), {q} queries over {s} values, 8 heads x 32, 4 levels x 4 points",
@@ -343,13 +368,13 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
         qq = torch.randn(bh, n, HD, device=dev, generator=g).half()
         tb = (0.02 * torch.randn(4 * side - 2, HD, device=dev, generator=g)).half()
         pr = torch.empty_like(sc)
-
-        def run():
-            check(lib, lib.sam_hip_relpos_softmax(sc.data_ptr(), qq.data_ptr(), tb.data_ptr(), pr.data_ptr(), 1,
-                                                  bh * n, side, side, HD, HD ** -0.5, sp))
-
-        ms = timer.avg_ms(run, 20)
         nbytes = 2.0 * bh * n * n * 2 + bh * n * HD * 2
+        run = Cycle(cold_sets(nbytes, sc, qq, pr),
+                    lambda sc_, qq_, pr_: check(lib, lib.sam_hip_relpos_softmax(
+                        sc_.data_ptr(), qq_.data_ptr(), tb.data_ptr(), pr_.data_ptr(), 1, bh * n, side, side, HD,
+                        HD ** -0.5, sp)))
+        ms = timer.avg_ms(run, 20)
+        del run
         res[f"vit_h_relpos_softmax_{name}_f16"] = {
             "workload": f"SAM ViT-H relpos_softmax over materialised scores, {bh} x {n} rows of {n}, hd {HD}, f16",
             "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
@@ -375,13 +400,12 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
             mean = (ctypes.c_float * 3)(*sam_hip.SAM_MEAN)
             std = (ctypes.c_float * 3)(*sam_hip.SAM_STD)
             code = CODE[dname]
-
-            def run():
-                check(lib, lib.sam_hip_preprocess(img.data_ptr(), out.data_ptr(), code, ih, iw, nh, nw, 1024, mean,
-                                                  std, sp))
-
-            ms = timer.avg_ms(run, 50)
             nbytes = float(ih * iw * 3 + 3 * 1024 * 1024 * out.element_size())
+            run = Cycle(cold_sets(nbytes, img, out),
+                        lambda im, o: check(lib, lib.sam_hip_preprocess(im.data_ptr(), o.data_ptr(), code, ih, iw, nh,
+                                                                        nw, 1024, mean, std, sp)))
+            ms = timer.avg_ms(run, 50)
+            del run
             res[f"preprocess_{name}_{dname}"] = {
                 "workload": f"SAM image preprocessing: u8 {iw}x{ih} RGB -> resize to {nw}x{nh} (antialiased), "
                             f"normalise, pad to 3x1024x1024 {dname}",
@@ -489,12 +513,12 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
         y = torch.randn(tok, 3 * 1280, device=dev, generator=g).half()
         bq = torch.randn(3 * 1280, device=dev, generator=g).half()
         packed = torch.empty(3, tok * 1280, device=dev, dtype=torch.float16)
-
-        def run():
-            check(lib, lib.sam_hip_qkv_split(y.data_ptr(), bq.data_ptr(), packed.data_ptr(), 1, tok, n, 16, 80, sp))
-
-        ms = timer.avg_ms(run, 50)
         nbytes = 2.0 * tok * 3 * 1280 * 2
+        run = Cycle(cold_sets(nbytes, y, packed),
+                    lambda y_, pk: check(lib, lib.sam_hip_qkv_split(y_.data_ptr(), bq.data_ptr(), pk.data_ptr(), 1, tok,
+                                                                    n, 16, 80, sp)))
+        ms = timer.avg_ms(run, 50)
+        del run
         res[f"vit_h_qkv_split_{name}_f16"] = {
             "workload": f"SAM ViT-H qkv_split, {tok} tokens ({n} per window) x 16 heads x 80, f16",
             "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
@@ -515,16 +539,18 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
         bvec = torch.randn(cols, device=dev, generator=g).half()
         out = torch.empty_like(y)
         if name == "bias_residual":
-            def run():
-                check(lib, lib.sam_hip_bias_residual(resid.data_ptr(), y.data_ptr(), bvec.data_ptr(), out.data_ptr(), 1,
-                                                     rows * cols, cols, sp))
             nbytes = 3.0 * rows * cols * 2
+            run = Cycle(cold_sets(nbytes, resid, y, out),
+                        lambda r_, y_, o: check(lib, lib.sam_hip_bias_residual(r_.data_ptr(), y_.data_ptr(),
+                                                                               bvec.data_ptr(), o.data_ptr(), 1,
+                                                                               rows * cols, cols, sp)))
         else:
-            def run():
-                check(lib, lib.sam_hip_bias_gelu(y.data_ptr(), bvec.data_ptr(), out.data_ptr(), 1, rows * cols, cols,
-                                                 sp))
             nbytes = 2.0 * rows * cols * 2
+            run = Cycle(cold_sets(nbytes, y, out),
+                        lambda y_, o: check(lib, lib.sam_hip_bias_gelu(y_.data_ptr(), bvec.data_ptr(), o.data_ptr(), 1,
+                                                                       rows * cols, cols, sp)))
         ms = timer.avg_ms(run, 50)
+        del run
         res[f"vit_h_{name}_f16"] = {
             "workload": f"SAM ViT-H {name} over {rows} tokens x {cols} channels, f16",
             "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,

@@ -9,8 +9,8 @@
 // bit-identical to it.
 //
 // One workgroup per (window, token tile, head), the tiles of a window balanced (196 tokens: 4 x 49).
-// A thread owns one token of the tile and every fourth 16-byte vector of its head's row, so the index
-// arithmetic has no division: q and v rows are copied with 16-byte accesses on both sides; the k part
+// A thread owns one token of the tile and every fourth 16-byte vector of its head's row (all of them
+// requested before the first store, for more bytes in flight), so the index arithmetic has no division: q and v rows are copied with 16-byte accesses on both sides; the k part
 // goes through an LDS tile so that kT is written as rows of consecutive tokens (up to 128 bytes in
 // f16) rather than 2-byte scatters. Bound by HBM: y is read once, out written once.
 //
@@ -23,7 +23,8 @@
 //
 // window_merge is the step after the attention: ctx [B*nW*nh, ws*ws, hd] in window order -> out
 // [B, gh, gw, nh*hd], heads merged (sam1/encoder.rs:83) and the windows put back on the grid without
-// their padding (window_unpartition, sam1/encoder.rs:140-143), one 16-byte vector per thread.
+// their padding (window_unpartition, sam1/encoder.rs:140-143), four 16-byte vectors per thread, all loaded
+// before the first is stored.
 #include "common.hpp"
 
 namespace samhip {
@@ -32,7 +33,10 @@ constexpr int kQkvTok = 64;     // tokens per tile at most
 constexpr int kQkvLanes = 4;    // threads per token row
 constexpr int kQkvThreads = kQkvTok * kQkvLanes;
 
-template <typename T, int VE>  // VE elements per vector access (16 bytes, or 1 when hd is odd-sized)
+// VE elements per vector access (16 bytes, or 1 when hd is not a multiple of 8); NV (VE == 8): a bound on the
+// vectors per thread and part, ceil(hd / 8 / kQkvLanes), so that every load of the thread is issued before the
+// first store (NV = 0: one vector at a time)
+template <typename T, int VE, int NV>
 __global__ __launch_bounds__(kQkvThreads) void qkv_split_kernel(const T* __restrict__ y, const T* __restrict__ bias,
                                                                T* __restrict__ out, int n, int nh, int hd, int tiles,
                                                                int tt, long plane, int gh, int gw, int ws) {
@@ -61,7 +65,41 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_split_kernel(const T* __restr
     const int i = n0 + tok, ti = i / ws, tj = i - ti * ws, r = wi * ws + ti, c = wj * ws + tj;
     t = r < gh && c < gw ? (wb * gh + r) * gw + c : -1;
   }
-  if (tok < ntok) {
+  if (NV > 0 && tok < ntok) {
+    // the token's q, k and v vectors of this head, all requested before any is used
+    const T* yrow = y + (t < 0 ? 0 : t) * 3L * C + head * hd;
+    V8 a[3][NV > 0 ? NV : 1];
+#pragma unroll
+    for (int which = 0; which < 3; ++which)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int v = lane + j * kQkvLanes;
+        a[which][j] = t < 0 || v >= vpr ? V8{} : *reinterpret_cast<const V8*>(yrow + which * C + v * 8);
+      }
+#pragma unroll
+    for (int which = 0; which < 3; ++which) {
+      const T* bsrc = bias + which * C + head * hd;
+      T* dst = out + which * plane + (bh * n + n0 + tok) * hd;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int v = lane + j * kQkvLanes;
+        if (v >= vpr) break;
+        const V8 bb = *reinterpret_cast<const V8*>(bsrc + v * 8);
+        float vals[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vals[e] = to_f32(a[which][j][e]) + to_f32(bb[e]);
+        if (which == 1) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) kt_tile[(v * 8 + e) * (kQkvTok + 1) + tok] = vals[e];
+        } else {
+          V8 o;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = from_f32<T>(vals[e]);
+          *reinterpret_cast<V8*>(dst + v * 8) = o;
+        }
+      }
+    }
+  } else if (tok < ntok) {
     const T* yrow = y + (t < 0 ? 0 : t) * 3L * C + head * hd;
 #pragma unroll
     for (int which = 0; which < 3; ++which) {
@@ -111,11 +149,21 @@ static hipError_t launch_qkv(const void* y, const void* bias, void* out, long to
   const long blocks = windows * tiles * nh;
   const long plane = tokens * nh * (long)hd;
   const size_t lds = (size_t)hd * (kQkvTok + 1) * sizeof(float);
-  if (hd % 8 == 0)
-    hipLaunchKernelGGL((qkv_split_kernel<T, 8>), dim3((unsigned)blocks), dim3(kQkvThreads), lds, stream,
+  const int nv = (hd / 8 + kQkvLanes - 1) / kQkvLanes;  // vectors per thread and part (hd % 8 == 0)
+  if (hd % 8 == 0 && nv <= 2)
+    hipLaunchKernelGGL((qkv_split_kernel<T, 8, 2>), dim3((unsigned)blocks), dim3(kQkvThreads), lds, stream,
+                       (const T*)y, (const T*)bias, (T*)out, n, nh, hd, tiles, tt, plane, gh, gw, ws);
+  else if (hd % 8 == 0 && nv == 3)
+    hipLaunchKernelGGL((qkv_split_kernel<T, 8, 3>), dim3((unsigned)blocks), dim3(kQkvThreads), lds, stream,
+                       (const T*)y, (const T*)bias, (T*)out, n, nh, hd, tiles, tt, plane, gh, gw, ws);
+  else if (hd % 8 == 0 && nv == 4)
+    hipLaunchKernelGGL((qkv_split_kernel<T, 8, 4>), dim3((unsigned)blocks), dim3(kQkvThreads), lds, stream,
+                       (const T*)y, (const T*)bias, (T*)out, n, nh, hd, tiles, tt, plane, gh, gw, ws);
+  else if (hd % 8 == 0)
+    hipLaunchKernelGGL((qkv_split_kernel<T, 8, 0>), dim3((unsigned)blocks), dim3(kQkvThreads), lds, stream,
                        (const T*)y, (const T*)bias, (T*)out, n, nh, hd, tiles, tt, plane, gh, gw, ws);
   else
-    hipLaunchKernelGGL((qkv_split_kernel<T, 1>), dim3((unsigned)blocks), dim3(kQkvThreads), lds, stream,
+    hipLaunchKernelGGL((qkv_split_kernel<T, 1, 0>), dim3((unsigned)blocks), dim3(kQkvThreads), lds, stream,
                        (const T*)y, (const T*)bias, (T*)out, n, nh, hd, tiles, tt, plane, gh, gw, ws);
   return hipGetLastError();
 }
@@ -139,24 +187,38 @@ hipError_t qkv_split_grid(int dtype, const void* y, const void* bias, void* out,
   return launch_qkv<bf16>(y, bias, out, tokens, n, nh, hd, stream, gh, gw, ws);
 }
 
+constexpr int kMergeVecs = 4;  // output vectors per thread, a block's width apart
+
 template <typename T, int VE>
 __global__ __launch_bounds__(256) void window_merge_kernel(const T* __restrict__ ctx, T* __restrict__ out, int gh,
                                                           int gw, int ws, int nh, int hd, long nvec) {
   typedef T TV __attribute__((ext_vector_type(VE)));
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= nvec) return;
   const int C = nh * hd;
-  const long e = i * VE;                   // output element: ((b*gh + r)*gw + c)*C + h*hd + d
-  const long tokc = e / C;
-  const int col = (int)(e - tokc * C), h = col / hd, d = col - h * hd;
-  const long bg = tokc / gw;
-  const int c = (int)(tokc - bg * gw);
-  const long b = bg / gh;
-  const int r = (int)(bg - b * gh);
   const int nww = (gw + ws - 1) / ws, nwh = (gh + ws - 1) / ws;
-  const long win = (b * nwh + r / ws) * nww + c / ws;
-  const int tok = (r % ws) * ws + c % ws;
-  *reinterpret_cast<TV*>(out + e) = *reinterpret_cast<const TV*>(ctx + ((win * nh + h) * ws * ws + tok) * hd + d);
+  const long i0 = (long)blockIdx.x * (256 * kMergeVecs) + threadIdx.x;
+  // every load of the thread is requested before the first store
+  TV v[kMergeVecs];
+#pragma unroll
+  for (int k = 0; k < kMergeVecs; ++k) {
+    const long i = i0 + 256L * k;
+    if (i >= nvec) break;
+    const long e = i * VE;  // output element: ((b*gh + r)*gw + c)*C + h*hd + d
+    const long tokc = e / C;
+    const int col = (int)(e - tokc * C), h = col / hd, d = col - h * hd;
+    const long bg = tokc / gw;
+    const int c = (int)(tokc - bg * gw);
+    const long b = bg / gh;
+    const int r = (int)(bg - b * gh);
+    const long win = (b * nwh + r / ws) * nww + c / ws;
+    const int tok = (r % ws) * ws + c % ws;
+    v[k] = *reinterpret_cast<const TV*>(ctx + ((win * nh + h) * ws * ws + tok) * hd + d);
+  }
+#pragma unroll
+  for (int k = 0; k < kMergeVecs; ++k) {
+    const long i = i0 + 256L * k;
+    if (i >= nvec) break;
+    *reinterpret_cast<TV*>(out + i * VE) = v[k];
+  }
 }
 
 template <typename T>
@@ -165,7 +227,7 @@ static hipError_t launch_merge(const void* ctx, void* out, int batch, int gh, in
   const long elems = (long)batch * gh * gw * nh * hd;
   const int ve = hd % (16 / (int)sizeof(T)) == 0 ? 16 / (int)sizeof(T) : (hd % 2 == 0 ? 2 : 1);
   const long nvec = elems / ve;
-  const unsigned blocks = (unsigned)((nvec + 255) / 256);
+  const unsigned blocks = (unsigned)((nvec + 256 * kMergeVecs - 1) / (256 * kMergeVecs));
   if (ve == 16 / (int)sizeof(T))
     hipLaunchKernelGGL((window_merge_kernel<T, 16 / sizeof(T)>), dim3(blocks), dim3(256), 0, stream, (const T*)ctx,
                        (T*)out, gh, gw, ws, nh, hd, nvec);
