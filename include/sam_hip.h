@@ -156,6 +156,21 @@ int sam_hip_bias_residual(const void* res, const void* y, const void* bias, void
 int sam_hip_bias_gelu(const void* y, const void* bias, void* out, int dtype, long total, int c, void* stream);
 
 /*
+ * bias_residual followed by LayerNorm over each row, in one pass: for rows of c elements,
+ *   out[r, :]    = res[r, :] + y[r, :] + bias          (as sam_hip_bias_residual, rounded to dtype)
+ *   ln_out[r, :] = (out[r, :] - mean) / sqrt(var + eps) * ln_w + ln_b   (biased variance, f32)
+ * with mean and var taken over the rounded out row. The reference runs the two as separate steps of
+ * its encoder block, kernels::bias_residual (kernels.rs:1040-1049) and candle_nn::LayerNorm
+ * (sam1/encoder.rs:118-124: the residual after the attention, then norm2; the residual after the MLP,
+ * then the next block's norm1); no single reference kernel corresponds to the pair. c must be a
+ * multiple of the 16-byte vector width (4 f32, 8 f16/bf16) and at most 512 vectors (2048 f32, 4096
+ * f16/bf16), every pointer 16-byte aligned; otherwise SAM_HIP_EUNSUPPORTED. out may alias res or y;
+ * ln_out must not alias any input.
+ */
+int sam_hip_bias_residual_ln(const void* res, const void* y, const void* bias, const void* ln_w, const void* ln_b,
+                             void* out, void* ln_out, int dtype, long rows, int c, float eps, void* stream);
+
+/*
  * Flash attention without a mask, f32 / f16 / bf16, on [b, l, h, d] operands given by (batch, row, head)
  * element strides (NULL = contiguous [b, l, h, d]; the head dimension is always contiguous):
  *   out[b, i, h, :] = softmax_j(scale * q[b,i,h,:] . k[b,j,h,:]) . v[b, :, h, :]

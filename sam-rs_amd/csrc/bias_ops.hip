@@ -5,6 +5,12 @@
 // then 0.5 * x * (1 + erf(x / sqrt(2))), the erf term through an erfc fit, see gelu_erf) and one
 // rounding to the output type.
 //
+//   bias_residual_ln: the same out, and also ln = LayerNorm(out) over each row of c (weight w, bias b,
+//   epsilon eps), from out as rounded to the output type: the two steps the encoder block runs one
+//   after the other (sam1/encoder.rs:118-124, a residual then the next norm), fused so that out is not
+//   read back. Mean and variance are two passes in f32 over the row held in registers, ln =
+//   ((x - mean) * rstd) * w + b in f32 with one rounding.
+//
 // out may be res or y (in place): each element is read and then written by the same thread.
 // Both are bound by HBM: each thread moves 16-byte vectors of every operand (4 f32 or 8 f16/bf16
 // elements; c a multiple of the vector width keeps a vector inside one bias period), in a grid-stride
@@ -95,6 +101,71 @@ __global__ __launch_bounds__(bias::kThreads) void bias_ops_kernel(const T* res, 
   }
 }
 
+// One wave per row of c elements, NV 16-byte vectors per lane at most (c <= 64 * NV * vector width).
+template <typename T, int NV>
+__global__ __launch_bounds__(bias::kThreads) void bias_residual_ln_kernel(
+    const T* res, const T* y, const T* __restrict__ b, const T* __restrict__ lw, const T* __restrict__ lb, T* out,
+    T* __restrict__ ln, long rows, int c, float eps) {
+#pragma clang fp contract(off)
+  typedef typename Vec16<T>::type V;
+  constexpr int n = Vec16<T>::n;
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * (bias::kThreads / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nv = c / n;
+  const long base = row * c;
+  float x[NV][n];
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int v = lane + 64 * j;
+    if (v < nv) {
+      const V rv = *reinterpret_cast<const V*>(res + base + v * n);
+      const V yv = *reinterpret_cast<const V*>(y + base + v * n);
+      const V bv = *reinterpret_cast<const V*>(b + v * n);
+      V o;
+#pragma unroll
+      for (int k = 0; k < n; ++k) {
+        o[k] = from_f32<T>(to_f32(rv[k]) + to_f32(yv[k]) + to_f32(bv[k]));
+        x[j][k] = to_f32(o[k]);
+        sum += x[j][k];
+      }
+      *reinterpret_cast<V*>(out + base + v * n) = o;
+    } else {
+#pragma unroll
+      for (int k = 0; k < n; ++k) x[j][k] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m);
+  const float mean = sum / (float)c;
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    if (lane + 64 * j < nv) {
+#pragma unroll
+      for (int k = 0; k < n; ++k) {
+        const float d = x[j][k] - mean;
+        sq += d * d;
+      }
+    }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) sq += __shfl_xor(sq, m);
+  const float rstd = 1.f / sqrtf(sq / (float)c + eps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int v = lane + 64 * j;
+    if (v < nv) {
+      const V wv = *reinterpret_cast<const V*>(lw + v * n);
+      const V bv = *reinterpret_cast<const V*>(lb + v * n);
+      V o;
+#pragma unroll
+      for (int k = 0; k < n; ++k) o[k] = from_f32<T>(((x[j][k] - mean) * rstd) * to_f32(wv[k]) + to_f32(bv[k]));
+      *reinterpret_cast<V*>(ln + base + v * n) = o;
+    }
+  }
+}
+
 template <typename T, int MODE>
 static hipError_t launch_bias(const void* res, const void* y, const void* b, void* out, long total, int c,
                               hipStream_t stream) {
@@ -120,6 +191,39 @@ hipError_t bias_residual(int dtype, const void* res, const void* y, const void* 
   if (dtype == kF32) return launch_bias<float, 0>(res, y, b, out, total, c, stream);
   if (dtype == kF16) return launch_bias<f16, 0>(res, y, b, out, total, c, stream);
   return launch_bias<bf16, 0>(res, y, b, out, total, c, stream);
+}
+
+template <typename T>
+static hipError_t launch_residual_ln(const void* res, const void* y, const void* b, const void* lw, const void* lb,
+                                     void* out, void* ln, long rows, int c, float eps, hipStream_t stream) {
+  const int nv = (c / Vec16<T>::n + 63) / 64;
+  const unsigned blocks = (unsigned)((rows + bias::kThreads / 64 - 1) / (bias::kThreads / 64));
+  if (rows <= 0) return hipSuccess;
+#define SAMHIP_RLN(NV)                                                                                          \
+  hipLaunchKernelGGL((bias_residual_ln_kernel<T, NV>), dim3(blocks), dim3(bias::kThreads), 0, stream,            \
+                     (const T*)res, (const T*)y, (const T*)b, (const T*)lw, (const T*)lb, (T*)out, (T*)ln, rows, c, \
+                     eps)
+  if (nv <= 1)
+    SAMHIP_RLN(1);
+  else if (nv <= 2)
+    SAMHIP_RLN(2);
+  else if (nv <= 3)
+    SAMHIP_RLN(3);
+  else if (nv <= 4)
+    SAMHIP_RLN(4);
+  else
+    SAMHIP_RLN(8);
+#undef SAMHIP_RLN
+  return hipGetLastError();
+}
+
+// Checked by the caller: rows >= 0, 1 <= c <= kResidualLnMax(dtype), c a multiple of the 16-byte vector
+// width, 16-byte aligned pointers.
+hipError_t bias_residual_ln(int dtype, const void* res, const void* y, const void* b, const void* lw, const void* lb,
+                            void* out, void* ln, long rows, int c, float eps, hipStream_t stream) {
+  if (dtype == kF32) return launch_residual_ln<float>(res, y, b, lw, lb, out, ln, rows, c, eps, stream);
+  if (dtype == kF16) return launch_residual_ln<f16>(res, y, b, lw, lb, out, ln, rows, c, eps, stream);
+  return launch_residual_ln<bf16>(res, y, b, lw, lb, out, ln, rows, c, eps, stream);
 }
 
 hipError_t bias_gelu(int dtype, const void* y, const void* b, void* out, long total, int c, hipStream_t stream) {

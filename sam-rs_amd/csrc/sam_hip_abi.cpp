@@ -34,6 +34,8 @@ int preprocess_max_taps(int n, int nout);
 hipError_t bias_residual(int dtype, const void* res, const void* y, const void* b, void* out, long total, int c,
                          hipStream_t stream);
 hipError_t bias_gelu(int dtype, const void* y, const void* b, void* out, long total, int c, hipStream_t stream);
+hipError_t bias_residual_ln(int dtype, const void* res, const void* y, const void* b, const void* lw, const void* lb,
+                            void* out, void* ln, long rows, int c, float eps, hipStream_t stream);
 }  // namespace samhip
 
 namespace {
@@ -181,6 +183,26 @@ int sam_hip_bias_residual(const void* res, const void* y, const void* bias, void
     return fail(SAM_HIP_EINVAL, "bias-residual: %ld elements do not hold whole rows of the %d-element bias", total, c);
   hipError_t e = samhip::bias_residual(dtype, res, y, bias, out, total, c, reinterpret_cast<hipStream_t>(stream));
   return check_launch(e, "bias-residual");
+}
+
+int sam_hip_bias_residual_ln(const void* res, const void* y, const void* bias, const void* ln_w, const void* ln_b,
+                             void* out, void* ln_out, int dtype, long rows, int c, float eps, void* stream) {
+  if (!res || !y || !bias || !ln_w || !ln_b || !out || !ln_out)
+    return fail(SAM_HIP_EINVAL, "bias-residual-ln: null pointer argument");
+  if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
+  const int vec = dtype == 0 ? 4 : 8;  // elements per 16-byte vector (f32: 4)
+  if (rows < 0 || c <= 0 || !(eps >= 0.f))
+    return fail(SAM_HIP_EINVAL, "bias-residual-ln: rows %ld, c %d, eps %g", rows, c, (double)eps);
+  if (c % vec != 0 || c > 512 * vec)
+    return fail(SAM_HIP_EUNSUPPORTED, "bias-residual-ln: the row length %d must be a multiple of %d and at most %d", c,
+                vec, 512 * vec);
+  if (rows > (1L << 40) / c) return fail(SAM_HIP_EINVAL, "bias-residual-ln: %ld rows of %d are too many", rows, c);
+  if (!aligned16(res) || !aligned16(y) || !aligned16(bias) || !aligned16(ln_w) || !aligned16(ln_b) ||
+      !aligned16(out) || !aligned16(ln_out))
+    return fail(SAM_HIP_EUNSUPPORTED, "bias-residual-ln: every pointer must be 16-byte aligned");
+  hipError_t e = samhip::bias_residual_ln(dtype, res, y, bias, ln_w, ln_b, out, ln_out, rows, c, eps,
+                                          reinterpret_cast<hipStream_t>(stream));
+  return check_launch(e, "bias-residual-ln");
 }
 
 int sam_hip_bias_gelu(const void* y, const void* bias, void* out, int dtype, long total, int c, void* stream) {

@@ -6,7 +6,9 @@ GELU) and the neck. Per block, the reference's kernel calls map to:
 - window_partition + qkv_split (encoder.rs:129-137, kernels.rs:872) -> sam_hip.qkv_split_grid;
 - attention_relpos / relpos_softmax + bmm (encoder.rs:79-82) -> sam_hip.attention_relpos (fused);
 - the head merge and window_unpartition (encoder.rs:83, 140-143) -> sam_hip.window_merge;
-- bias_residual (kernels.rs:1040) -> sam_hip.bias_residual;
+- bias_residual (kernels.rs:1040) and the LayerNorm after it (the block's norm2, or the next
+  block's norm1) -> sam_hip.bias_residual_ln, one pass; the last block's bias_residual ->
+  sam_hip.bias_residual;
 - bias_gelu (kernels.rs:1052) -> sam_hip.bias_gelu.
 
 The linears run as torch's F.linear (hipBLASLt) and LayerNorm as torch's layer_norm. Their weights
@@ -149,15 +151,18 @@ def attention(x: torch.Tensor, p: BlockWeights, heads: int) -> torch.Tensor:
     return F.linear(out, p.proj_w).view(b, h, w, c)
 
 
-def block(x: torch.Tensor, p: BlockWeights, heads: int) -> torch.Tensor:
-    """encoder.rs:112-126."""
+def block(x: torch.Tensor, xn: torch.Tensor, p: BlockWeights, heads: int, nxt: BlockWeights = None):
+    """encoder.rs:112-126: x and xn = norm1(x) -> the block's output and, when a next block follows,
+    its norm1 of that output (each residual and the norm after it run as one pass)."""
     b, h, w, c = x.shape
-    y = attention(F.layer_norm(x, (c,), p.norm1_w, p.norm1_b, 1e-6), p, heads)
-    x = sam_hip.bias_residual(x, y, p.proj_b)
+    y = attention(xn, p, heads)
+    x, xn2 = sam_hip.bias_residual_ln(x, y, p.proj_b, p.norm2_w, p.norm2_b, 1e-6)
     t = b * h * w
-    m = sam_hip.bias_gelu(F.linear(F.layer_norm(x, (c,), p.norm2_w, p.norm2_b, 1e-6).reshape(t, c), p.lin1_w),
-                          p.lin1_b)
-    return sam_hip.bias_residual(x, F.linear(m, p.lin2_w).view(b, h, w, c), p.lin2_b)
+    m = sam_hip.bias_gelu(F.linear(xn2.reshape(t, c), p.lin1_w), p.lin1_b)
+    y = F.linear(m, p.lin2_w).view(b, h, w, c)
+    if nxt is None:
+        return sam_hip.bias_residual(x, y, p.lin2_b), None
+    return sam_hip.bias_residual_ln(x, y, p.lin2_b, nxt.norm1_w, nxt.norm1_b, 1e-6)
 
 
 def encoder_forward(img: torch.Tensor, w: EncoderWeights) -> torch.Tensor:
@@ -167,8 +172,9 @@ def encoder_forward(img: torch.Tensor, w: EncoderWeights) -> torch.Tensor:
     g, k, c = s // cfg.patch, cfg.patch, cfg.embed_dim
     patches = img.view(b, 3, g, k, g, k).permute(0, 2, 4, 1, 3, 5).reshape(b * g * g, 3 * k * k)
     x = (F.linear(patches, w.patch_w) + w.patch_b).view(b, g, g, c) + w.pos
-    for p in w.blocks:
-        x = block(x, p, cfg.heads)
+    xn = F.layer_norm(x, (c,), w.blocks[0].norm1_w, w.blocks[0].norm1_b, 1e-6)
+    for i, p in enumerate(w.blocks):
+        x, xn = block(x, xn, p, cfg.heads, w.blocks[i + 1] if i + 1 < len(w.blocks) else None)
     o = cfg.out_chans
     y = F.linear(x.reshape(b * g * g, c), w.neck0_w)  # 1x1 conv, tokens x out
     y = F.layer_norm(y, (o,), w.neck1_w, w.neck1_b, 1e-6)  # LayerNorm2d over channels

@@ -55,6 +55,8 @@ def load():
         L.sam_hip_bias_residual.restype = _i
         L.sam_hip_bias_gelu.argtypes = [_vp] * 3 + [_i, ctypes.c_long, _i, _vp]
         L.sam_hip_bias_gelu.restype = _i
+        L.sam_hip_bias_residual_ln.argtypes = [_vp] * 7 + [_i, ctypes.c_long, _i, ctypes.c_float, _vp]
+        L.sam_hip_bias_residual_ln.restype = _i
         _fp = ctypes.POINTER(ctypes.c_float)
         L.sam_hip_preprocess.argtypes = [_vp, _vp] + [_i] * 6 + [_fp, _fp, _vp]
         L.sam_hip_preprocess.restype = _i
@@ -195,6 +197,28 @@ def bias_residual(res: torch.Tensor, y: torch.Tensor, bias: torch.Tensor) -> tor
     _check(load().sam_hip_bias_residual(res.data_ptr(), y.data_ptr(), bias.data_ptr(), out.data_ptr(), dt,
                                         res.numel(), bias.numel(), _stream()))
     return out
+
+
+def bias_residual_ln(res: torch.Tensor, y: torch.Tensor, bias: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor,
+                     eps: float = 1e-6):
+    """bias_residual (kernels.rs:1040-1049) and then LayerNorm over the last dimension of its result
+    (candle_nn::LayerNorm as the encoder block applies it after each residual, sam1/encoder.rs:118-124),
+    in one pass: -> (x = res + y + bias, LayerNorm(x) * ln_w + ln_b), the norm taken over x as rounded
+    to the dtype."""
+    res, y, bias, ln_w, ln_b = (t.contiguous() for t in (res, y, bias, ln_w, ln_b))
+    _contig(res, y, bias, ln_w, ln_b)
+    dt = _dtype(res, y, bias, ln_w, ln_b)
+    c = res.shape[-1]
+    if res.shape != y.shape:
+        raise SamHipError(f"bias-residual-ln: shape mismatch {tuple(res.shape)} vs {tuple(y.shape)}")
+    if any(t.shape != (c,) for t in (bias, ln_w, ln_b)):
+        raise SamHipError(f"bias-residual-ln: bias, ln_w and ln_b must be [{c}], got "
+                          f"{[tuple(t.shape) for t in (bias, ln_w, ln_b)]}")
+    out, ln = torch.empty_like(res), torch.empty_like(res)
+    _check(load().sam_hip_bias_residual_ln(res.data_ptr(), y.data_ptr(), bias.data_ptr(), ln_w.data_ptr(),
+                                           ln_b.data_ptr(), out.data_ptr(), ln.data_ptr(), dt, res.numel() // c, c,
+                                           eps, _stream()))
+    return out, ln
 
 
 def bias_gelu(y: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:

@@ -7,6 +7,11 @@ and the formula amplifies that for negative inputs, so gelu is held to a relativ
 floor (below). Cases: the ViT-H shapes (tokens x
 1280 after attention, tokens x 5120 in the MLP), odd channel counts that take the scalar loop,
 misaligned views, in-place use and the argument errors.
+
+bias_residual_ln fuses bias_residual with the LayerNorm that follows it in an encoder block: its x is
+held bit for bit to the oracle's bias_residual rounded to the dtype, and its norm to a float64
+LayerNorm of that rounded x (mean, biased variance, (x - mean) / sqrt(var + eps) * w + b) within one
+rounding step of the dtype (f32: 10^-5 relative), with a 10^-5 absolute floor.
 """
 import numpy as np
 import pytest
@@ -92,3 +97,57 @@ def test_bias_op_errors(hip):
     assert lib.sam_hip_bias_gelu(x.data_ptr(), x.data_ptr(), x.data_ptr(), 0, 24, 5, None) == 1
     assert b"whole rows" in lib.sam_hip_last_error()
     assert lib.sam_hip_bias_gelu(x.data_ptr(), x.data_ptr(), x.data_ptr(), 0, 0, 6, None) == 0  # empty
+
+
+LN_SHAPES = [(4096, 1280), (2, 33, 768), (3, 1024), (5, 8), (2, 2048), (7, 4)]
+LN_RTOL = {"f32": 1e-5, "f16": 2.0 ** -10, "bf16": 2.0 ** -7}
+
+
+def ln_want(res, y, b, w, lb, dtype, eps):
+    x = oracle.round_to(oracle.bias_residual(res, y, b), dtype)
+    x64 = x.astype(np.float64)
+    mean = x64.mean(-1, keepdims=True)
+    var = ((x64 - mean) ** 2).mean(-1, keepdims=True)
+    return x, (x64 - mean) / np.sqrt(var + eps) * w.astype(np.float64) + lb.astype(np.float64)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("shape", LN_SHAPES, ids=["x".join(map(str, s)) for s in LN_SHAPES])
+def test_bias_residual_ln_matches_float64_layer_norm(hip, shape, dtype):
+    c = shape[-1]
+    if dtype == "f32" and c % 4 or dtype != "f32" and c % 8:
+        pytest.skip("row length not a multiple of the vector width")
+    print(f"bias_residual_ln {shape} {dtype}", flush=True)
+    res, y = data(shape, 21, dtype), data(shape, 22, dtype, 0.5)
+    b = data((c,), 23, dtype, 0.1)
+    w = oracle.round_to(1.0 + 0.2 * np.random.default_rng(24).standard_normal(c).astype(np.float32), dtype)
+    lb = data((c,), 25, dtype, 0.1)
+    x_want, ln64 = ln_want(res, y, b, w, lb, dtype, 1e-6)
+    x, ln = hip.bias_residual_ln(dev(res, dtype), dev(y, dtype), dev(b, dtype), dev(w, dtype), dev(lb, dtype), 1e-6)
+    assert np.array_equal(x.float().cpu().numpy(), x_want)
+    got = ln.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - ln64)
+    assert (err <= LN_RTOL[dtype] * np.abs(ln64) + 1e-5).all(), err.max()
+
+
+def test_bias_residual_ln_in_place_and_errors(hip):
+    res = torch.randn(64, 1280, device="cuda").half()
+    y = torch.randn(64, 1280, device="cuda").half()
+    b, w, lb = (torch.randn(1280, device="cuda").half() for _ in range(3))
+    x_ref, ln_ref = hip.bias_residual_ln(res, y, b, w, lb)
+    lib = hip.load()
+    r2, ln2 = res.clone(), torch.empty_like(res)
+    # out over res: every element is read and then written by the same thread
+    assert lib.sam_hip_bias_residual_ln(r2.data_ptr(), y.data_ptr(), b.data_ptr(), w.data_ptr(), lb.data_ptr(),
+                                        r2.data_ptr(), ln2.data_ptr(), 1, 64, 1280, 1e-6, hip._stream()) == 0
+    assert torch.equal(r2, x_ref) and torch.equal(ln2, ln_ref)
+    args = [r2.data_ptr(), y.data_ptr(), b.data_ptr(), w.data_ptr(), lb.data_ptr(), r2.data_ptr(), ln2.data_ptr()]
+    assert lib.sam_hip_bias_residual_ln(*args, 1, 64 * 1280 // 1284, 1284, 1e-6, None) == 3  # not whole vectors
+    assert b"multiple of 8" in lib.sam_hip_last_error()
+    assert lib.sam_hip_bias_residual_ln(*args, 1, 1, 8192, 1e-6, None) == 3  # longer than 512 vectors
+    assert lib.sam_hip_bias_residual_ln(*args, 1, 64, 1280, -1.0, None) == 1  # negative eps
+    mis = args[:]
+    mis[1] = y.data_ptr() + 2
+    assert lib.sam_hip_bias_residual_ln(*mis, 1, 63, 1280, 1e-6, None) == 3
+    assert b"16-byte aligned" in lib.sam_hip_last_error()
+    assert lib.sam_hip_bias_residual_ln(*args, 1, 0, 1280, 1e-6, None) == 0  # no rows
