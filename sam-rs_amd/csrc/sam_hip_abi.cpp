@@ -196,7 +196,9 @@ int sam_hip_bias_residual_ln(const void* res, const void* y, const void* bias, c
   if (c % vec != 0 || c > 512 * vec)
     return fail(SAM_HIP_EUNSUPPORTED, "bias-residual-ln: the row length %d must be a multiple of %d and at most %d", c,
                 vec, 512 * vec);
-  if (rows > (1L << 40) / c) return fail(SAM_HIP_EINVAL, "bias-residual-ln: %ld rows of %d are too many", rows, c);
+  // elements below 2^40; one wave per row, four rows per workgroup, fewer than 2^31 workgroups
+  if (rows > (1L << 40) / c || rows > 4L * 0x7fffffffL)
+    return fail(SAM_HIP_EUNSUPPORTED, "bias-residual-ln: %ld rows of %d are too many", rows, c);
   if (!aligned16(res) || !aligned16(y) || !aligned16(bias) || !aligned16(ln_w) || !aligned16(ln_b) ||
       !aligned16(out) || !aligned16(ln_out))
     return fail(SAM_HIP_EUNSUPPORTED, "bias-residual-ln: every pointer must be 16-byte aligned");
