@@ -117,7 +117,8 @@ def test_relpos_softmax_rejects_long_rows(hip):
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("n,nh,hd,win", [(196, 12, 64, 3), (196, 16, 80, 25), (4096, 16, 80, 1), (77, 3, 8, 2),
-                                         (5, 2, 6, 3), (130, 1, 256, 2), (64, 4, 16, 2), (65, 2, 24, 1)])
+                                         (5, 2, 6, 3), (130, 1, 256, 2), (64, 4, 16, 2), (65, 2, 24, 1),
+                                         (50, 2, 128, 2)])
 def test_qkv_split_is_bit_exact(hip, n, nh, hd, win, dtype):
     print(f"qkv_split {dtype} n={n} nh={nh} hd={hd} win={win}", flush=True)
     r = np.random.default_rng(n + hd)
@@ -164,7 +165,7 @@ def test_qkv_split_grid_equals_partition_then_split(hip, batch, gh, gw, ws, nh, 
         assert np.array_equal(a.float().cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("batch,gh,gw,ws,nh,hd", GRID_SHAPES)
 def test_window_merge_is_unpartition_of_merged_heads(hip, batch, gh, gw, ws, nh, hd, dtype):
     """window_merge(ctx) = window_unpartition (sam1/encoder.rs:140-143) of the heads merged as
