@@ -31,6 +31,7 @@ GLOBAL_LAYERS = (7, 15, 23, 31)
 DEPTH, HEADS, HD = 32, 16, 80
 WINDOWS = 25  # 64x64 tokens padded to 70x70 -> 5 x 5 windows of 14x14
 CODE = {"f32": 0, "f16": 1, "bf16": 2}
+WARM_MS = 100.0  # minimum GPU time of the headline's warmup, whatever --warmup says
 
 
 def parse():
@@ -290,6 +291,34 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
             f"one layer's self ({ts:.3f} s) and cross ({tc:.3f} s) attention in f32 (the reference's CPU sdpa), "
             "scaled by 4 layers")
     del layers, ws
+
+    # The ViT-H attention layers of the headline in bf16 (batch 1): the global layer (16 heads x 64x64) on
+    # the bf16 MFMA, and a windowed layer (400 units x 14x14), each on fresh operand sets so that every
+    # call reads its inputs from HBM, as the headline's layers do.
+    for name, (bh, side) in (("global", (HEADS, 64)), ("window", (WINDOWS * HEADS, 14))):
+        n = side * side
+        qb = torch.randn(bh, n, HD, device=dev, generator=g).bfloat16()
+        ktb = torch.randn(bh, HD, n, device=dev, generator=g).bfloat16()
+        vb = torch.randn(bh, n, HD, device=dev, generator=g).bfloat16()
+        tb = (0.02 * torch.randn(4 * side - 2, HD, device=dev, generator=g)).bfloat16()
+        ob = torch.empty_like(qb)
+        nbytes = window_bytes(bh, n)
+        run = Cycle(cold_sets(nbytes, qb, ktb, vb, ob),
+                    lambda q_, k_, v_, o_: check(lib, lib.sam_hip_attn_relpos(
+                        q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), tb.data_ptr(), o_.data_ptr(), 2, bh, side, side,
+                        HD, HD ** -0.5, sp)))
+        ms = timer.avg_ms(run, 40 if name == "global" else 200, warm_s=0.1)
+        del run
+        f = flops(bh, n)
+        leg = {"workload": f"SAM ViT-H {name} attention layer, bf16, batch 1: {bh} x {side}x{side}, hd {HD}",
+               "us": round(ms * 1e3, 2), "tflops": round(f / (ms * 1e-3) / 1e12, 1)}
+        if name == "global":
+            leg["frac_of_bf16_mfma_peak"] = round(f / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["bf16"], 4)
+        else:
+            leg["gbs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+            leg["frac_of_hbm_peak"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        res[f"vit_h_{name}_layer_bf16"] = leg
+        del qb, ktb, vb, ob
 
     # Grounding DINO-tiny deformable attention, f32: 4 levels of an 800x1333 input, 8 heads x 32, 4 points.
     shapes = [(100, 167), (50, 84), (25, 42), (13, 21)]
@@ -592,7 +621,10 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
             res[f"vit_b_{name}_f32"]["cpu_baseline"] = cpu_leg(
                 tcpu, 1, 1e6, "us", "the whole layer on the reference's exact-f32 TiledAttention branch "
                                     "(kernels.rs:181-220), best of 2")
-    return res
+    late = [k for k in ("dino_deform_core_decoder_f32", "dino_deform_decoder_f32", "dino_deform_core_encoder_f32",
+                        "dino_deform_encoder_f32", "sam2_memory_attention_f16", "vit_h_window_layer_bf16",
+                        "vit_h_global_layer_bf16") if k in res]
+    return {**{k: v for k, v in res.items() if k not in late}, **{k: res[k] for k in late}}
 
 
 def copy_probe(torch):
@@ -653,9 +685,26 @@ def main():
             if keep(i):
                 launch(L)
 
+    # Warmup: the given number of steps, then more until at least WARM_MS of GPU time has passed since
+    # the first. The chip reaches its steady clock only after tens of milliseconds of load, so a fixed
+    # small step count would time part of the clock ramp.
+    w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0.record(stream)
+    warm_steps = 0
     for _ in range(args.warmup):
         step()
+        warm_steps += 1
+    w1.record(stream)
     torch.cuda.synchronize()
+    warm_ms = w0.elapsed_time(w1)
+    while warm_ms < WARM_MS:
+        per_step = warm_ms / max(warm_steps, 1)
+        for _ in range(1 + int((WARM_MS - warm_ms) / max(per_step, 1e-3))):
+            step()
+            warm_steps += 1
+        w1.record(stream)
+        torch.cuda.synchronize()
+        warm_ms = w0.elapsed_time(w1)
     # The timed region: plain steps, bracketed by events on the launch stream. Events between the layers
     # would put host calls and queue markers between the kernels and lengthen the step by about a
     # quarter, so the per-kernel durations come from a second region right after it.
@@ -709,6 +758,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warm_steps,
+        "warmup_ms": round(warm_ms, 1),
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": False,
         "scaling": "weak",
@@ -739,10 +790,12 @@ def main():
         "window_layer_hbm_frac": round(win_gbs / HBM_PEAK_GBS, 4),
         "encoder_tflops": round(total_flops / (ms_step * 1e-3) / 1e12, 1),
     }
-    if not args.no_secondary:
-        line["secondary"] = secondary(torch, sam_hip, lib, dev, sp, Timer(torch, stream), cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
+    if not args.no_secondary:
+        # last on the line, with the legs of the path's other kernels at its very end, so that a reader of
+        # the line's tail sees them
+        line["secondary"] = secondary(torch, sam_hip, lib, dev, sp, Timer(torch, stream), cpu=not args.no_cpu_baseline)
     print(json.dumps(line), flush=True)
 
 

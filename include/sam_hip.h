@@ -26,8 +26,22 @@ enum sam_hip_status {
   SAM_HIP_EINVAL = 1,      /* a null pointer or an inconsistent size */
   SAM_HIP_EDTYPE = 2,      /* dtype not in {0, 1, 2} or not supported by this entry point */
   SAM_HIP_EUNSUPPORTED = 3, /* a shape beyond this kernel's limits (message says which) */
-  SAM_HIP_EHIP = 4         /* the HIP runtime reported an error at launch */
+  SAM_HIP_EHIP = 4,        /* the HIP runtime reported an error at launch */
+  SAM_HIP_EDISABLED = 5    /* the HIP path is switched off (sam_hip_set_enabled); nothing was done */
 };
+
+/*
+ * Process-wide switch of the HIP path, the counterpart of the reference's cpu_gemm::set_enabled /
+ * cpu_gemm::enabled (cpu_gemm.rs:11, 25-32), which main.rs:117-125 turns off for --f32. On by default;
+ * off from load time when the environment variable SAM_HIP_DISABLE is set to anything but "" or "0".
+ * While it is off, every compute entry point (all but the size queries, sam_hip_last_error,
+ * sam_hip_abi_version and these two) returns SAM_HIP_EDISABLED before reading any argument or
+ * touching a device, and the caller takes the reference's own path: the Rust binding maps that code
+ * to Ok(None) in the Option-returning ops and to the tensor path elsewhere. Takes effect for calls
+ * that start after it returns; safe to call from any thread.
+ */
+void sam_hip_set_enabled(int on);
+int sam_hip_enabled(void);
 
 /*
  * Fused SAM ViT attention with the decomposed relative-position bias:
@@ -219,7 +233,9 @@ int sam_hip_sdpa_mask(const void* q, const void* k, const void* v, const void* m
  * in the reference: its GPU flash attention allocates internally. The workspace comes from a fixed
  * array of SAM_HIP_FLASH_NOALLOC_MAX_BYTES bytes that the library holds on every GPU it runs on until
  * the process ends; a call whose sam_hip_flash_attn_workspace_size exceeds it fails with
- * SAM_HIP_EUNSUPPORTED (SAM 2.1 memory attention needs at most 65.3 MB on 256 CUs). The call itself
+ * SAM_HIP_EUNSUPPORTED. Its key-split plan assumes at most 256 CUs whatever the device has (the split
+ * count, and so the workspace, grows with the CU count), so a call's need does not depend on the
+ * device: SAM 2.1 memory attention needs 65.3 MB. The call itself
  * allocates nothing. All calls on one GPU share that array: calls on one stream are ordered and safe,
  * calls that overlap on one GPU (several streams or threads) race. Arguments and limits otherwise as
  * sam_hip_flash_attn.

@@ -205,34 +205,45 @@ static void softmax_div(float* x, int n) {
  *     ncoord 2 (encoder, :169-173): loc = ref + off / (W_l, H_l);
  *     ncoord 4 (decoder, :174-178): loc = xy + ((off * (1/p)) * wh) * 0.5, where candle's `off / p`
  *       is Tensor::affine(1/p, 0) (x * mul + add) and `.affine(0.5, 0.0)` is x * 0.5 + 0.
- * Every step is one f32 rounding, left to right, as the candle ops compute them. */
+ * Every step is one f32 rounding, left to right, as the candle ops compute them. The candle ops run in
+ * the query's dtype, so with round_dt 1 (f16) or 2 (bf16) each step's result, the softmax output and
+ * the level sizes (`norm`, converted with to_dtype at :170) are also rounded to that dtype. */
+static float round_bf16_scalar(float x);
+static float round_to_f16(float x);
+static float round_dt_scalar(float x, int dt) {
+  return dt == 1 ? round_to_f16(x) : dt == 2 ? round_bf16_scalar(x) : x;
+}
+
 void oracle_deform_prep(const float* off, const float* logits, const float* refs, float* loc, float* attn, int b,
-                        int q, int h, int l, int p, int ncoord, const int* shapes, int nthreads) {
+                        int q, int h, int l, int p, int ncoord, const int* shapes, int round_dt, int nthreads) {
   const long pairs = (long)b * q * h;
   const int npt = l * p;
   const float inv_p = (float)(1.0 / (double)p);
+#define R(x) round_dt_scalar((x), round_dt)
 #pragma omp parallel for schedule(static) num_threads(threads_or_all(nthreads))
   for (long pr = 0; pr < pairs; ++pr) {
     const long bq = pr / h;
     float* a = attn + pr * npt;
     for (int j = 0; j < npt; ++j) a[j] = logits[pr * npt + j];
     softmax_div(a, npt);
+    for (int j = 0; j < npt; ++j) a[j] = R(a[j]);
     for (int j = 0; j < npt; ++j) {
       const int li = j / p;
       const float* r = refs + (bq * l + li) * ncoord;
       const float ox = off[(pr * npt + j) * 2], oy = off[(pr * npt + j) * 2 + 1];
       float* o = loc + (pr * npt + j) * 2;
       if (ncoord == 2) {
-        o[0] = r[0] + ox / (float)shapes[2 * li + 1];
-        o[1] = r[1] + oy / (float)shapes[2 * li];
+        o[0] = R(r[0] + R(ox / R((float)shapes[2 * li + 1])));
+        o[1] = R(r[1] + R(oy / R((float)shapes[2 * li])));
       } else {
-        const float tx = ox * inv_p + 0.0f, ty = oy * inv_p + 0.0f;
-        const float ux = tx * r[2], uy = ty * r[3];
-        o[0] = r[0] + (ux * 0.5f + 0.0f);
-        o[1] = r[1] + (uy * 0.5f + 0.0f);
+        const float tx = R(ox * inv_p + 0.0f), ty = R(oy * inv_p + 0.0f);
+        const float ux = R(tx * r[2]), uy = R(ty * r[3]);
+        o[0] = R(r[0] + R(ux * 0.5f + 0.0f));
+        o[1] = R(r[1] + R(uy * 0.5f + 0.0f));
       }
     }
   }
+#undef R
 }
 
 void oracle_sdpa(const float* q, const float* k, const float* v, float* out, int b, int h, int lq, int lk, int d,
@@ -480,17 +491,21 @@ void oracle_round_f16(float* x, long n) {
   for (long i = 0; i < n; ++i) x[i] = round_to_f16(x[i]);
 }
 
-void oracle_round_bf16(float* x, long n) {
-  for (long i = 0; i < n; ++i) {
-    uint32_t b;
-    memcpy(&b, &x[i], 4);
-    if (isnan(x[i])) {
-      b = (b | 0x00400000u) & 0xffff0000u;
-    } else {
-      b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
-    }
-    memcpy(&x[i], &b, 4);
+/* bfloat16 round-to-nearest-even (NaN stays NaN), returned as f32. */
+static float round_bf16_scalar(float x) {
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  if (isnan(x)) {
+    b = (b | 0x00400000u) & 0xffff0000u;
+  } else {
+    b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
   }
+  memcpy(&x, &b, 4);
+  return x;
+}
+
+void oracle_round_bf16(float* x, long n) {
+  for (long i = 0; i < n; ++i) x[i] = round_bf16_scalar(x[i]);
 }
 
 static uint64_t splitmix64(uint64_t* st) {

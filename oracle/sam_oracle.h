@@ -47,7 +47,7 @@ void oracle_deform_attn(const float* value, const float* loc, const float* attn,
  * over l*p -> attn; offsets off [b,q,h,l,p,2] and refs [b,q,l,ncoord] (ncoord 2: encoder, 4: decoder)
  * -> loc [b,q,h,l,p,2]; shapes = l (height,width) pairs. */
 void oracle_deform_prep(const float* off, const float* logits, const float* refs, float* loc, float* attn, int b,
-                        int q, int h, int l, int p, int ncoord, const int* shapes, int nthreads);
+                        int q, int h, int l, int p, int ncoord, const int* shapes, int round_dt, int nthreads);
 
 /* sam3/nn.rs:26-34 (sdpa, mask = None) on [b, h, l, d] tensors: softmax(q k^T * d^-0.5) v. */
 void oracle_sdpa(const float* q, const float* k, const float* v, float* out, int b, int h, int lq, int lk, int d,

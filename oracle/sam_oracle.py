@@ -42,7 +42,7 @@ def lib():
         L.oracle_qkv_split.argtypes = [_F, _F, _F, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_int]
         L.oracle_deform_attn.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 7 + [_I, ctypes.c_int]
-        L.oracle_deform_prep.argtypes = [_F] * 5 + [ctypes.c_int] * 6 + [_I, ctypes.c_int]
+        L.oracle_deform_prep.argtypes = [_F] * 5 + [ctypes.c_int] * 6 + [_I, ctypes.c_int, ctypes.c_int]
         L.oracle_sdpa.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 6
         L.oracle_sdpa_mask.argtypes = [_F, _F, _F, _F, ctypes.POINTER(ctypes.c_long), _F] + [ctypes.c_int] * 6
         L.oracle_mha_blhd.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int]
@@ -121,8 +121,13 @@ def deform_attn(value, loc, attn, shapes, nthreads: int = 0) -> np.ndarray:
     return out
 
 
-def deform_prep(off, logits, refs, shapes, nthreads: int = 0):
-    """dino/mod.rs:166-178. off [B,Q,H,L,P,2], logits [B,Q,H,L,P], refs [B,Q,L,2|4] -> (loc, attn)."""
+_ROUND_DT = {"f32": 0, "f16": 1, "bf16": 2}
+
+
+def deform_prep(off, logits, refs, shapes, nthreads: int = 0, dtype: str = "f32"):
+    """dino/mod.rs:166-178. off [B,Q,H,L,P,2], logits [B,Q,H,L,P], refs [B,Q,L,2|4] -> (loc, attn).
+    dtype "f16" / "bf16": the candle ops run in that dtype, so every step's result (and the softmax
+    output) is rounded to it, as the reference computes them for a query of that dtype."""
     off, logits, refs = _f32(off), _f32(logits), _f32(refs)
     b, q, h, l, p, two = off.shape
     nc = refs.shape[-1]
@@ -132,13 +137,14 @@ def deform_prep(off, logits, refs, shapes, nthreads: int = 0):
     loc = np.empty_like(off)
     attn = np.empty_like(logits)
     lib().oracle_deform_prep(_p(off), _p(logits), _p(refs), _p(loc), _p(attn), b, q, h, l, p, nc,
-                             sh.ctypes.data_as(_I), nthreads)
+                             sh.ctypes.data_as(_I), _ROUND_DT[dtype], nthreads)
     return loc, attn
 
 
-def deform_forward_core(value, off, logits, refs, shapes, nthreads: int = 0) -> np.ndarray:
-    """Deform::forward between its projections (dino/mod.rs:166-179): deform_prep, then deform_attn."""
-    loc, attn = deform_prep(off, logits, refs, shapes, nthreads)
+def deform_forward_core(value, off, logits, refs, shapes, nthreads: int = 0, dtype: str = "f32") -> np.ndarray:
+    """Deform::forward between its projections (dino/mod.rs:166-179): deform_prep (its steps rounded to
+    `dtype`), then deform_attn (which reads loc and attn as the dtype's values and computes in f32)."""
+    loc, attn = deform_prep(off, logits, refs, shapes, nthreads, dtype)
     return deform_attn(value, loc, attn, shapes, nthreads)
 
 

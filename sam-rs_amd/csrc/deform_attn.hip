@@ -74,7 +74,17 @@ __device__ __forceinline__ void pair_softmax(const T* logits, long base0, int np
 // Point j (level l) of pair `pair` (bq = b * Q + q): normalised location (x, y) and weight w.
 // NC = 2 (encoder, dino/mod.rs:169-173): loc = ref + off / (W_l, H_l).
 // NC = 4 (decoder, dino/mod.rs:174-178): loc = xy + ((off * (1/P)) * wh) * 0.5.
-// Each step is one f32 rounding, as the reference's tensor ops are (no contraction).
+// Each step is one f32 rounding, as the reference's tensor ops are (no contraction). Those ops run in
+// the query's dtype, so for f16 / bf16 each step's result, the softmax output and the level sizes (the
+// `norm` tensor, converted to the dtype at :170) are rounded to T as well.
+template <typename T>
+__device__ __forceinline__ float round_t(float x) {
+  if constexpr (__is_same(T, float))
+    return x;
+  else
+    return to_f32(from_f32<T>(x));
+}
+
 template <typename T, int NC>
 __device__ __forceinline__ void point_xyw(const PointSrc<T>& src, long pair, long bq, int npt, int j, int l, int L,
                                           int Wl, int Hl, float mx, float sum, float& x, float& y, float& w) {
@@ -86,15 +96,16 @@ __device__ __forceinline__ void point_xyw(const PointSrc<T>& src, long pair, lon
     x = ax;
     y = ay;
   } else {
-    w = expf(to_f32(src.attn[base]) - mx) / sum;
+    w = round_t<T>(expf(to_f32(src.attn[base]) - mx) / sum);
     const T* r = src.refs + (bq * L + l) * NC;
     if constexpr (NC == 2) {
-      x = to_f32(r[0]) + ax / (float)Wl;
-      y = to_f32(r[1]) + ay / (float)Hl;
+      x = round_t<T>(to_f32(r[0]) + round_t<T>(ax / round_t<T>((float)Wl)));
+      y = round_t<T>(to_f32(r[1]) + round_t<T>(ay / round_t<T>((float)Hl)));
     } else {
-      const float ux = (ax * src.inv_p) * to_f32(r[2]), uy = (ay * src.inv_p) * to_f32(r[3]);
-      x = to_f32(r[0]) + ux * 0.5f;
-      y = to_f32(r[1]) + uy * 0.5f;
+      const float ux = round_t<T>(round_t<T>(ax * src.inv_p) * to_f32(r[2]));
+      const float uy = round_t<T>(round_t<T>(ay * src.inv_p) * to_f32(r[3]));
+      x = round_t<T>(to_f32(r[0]) + round_t<T>(ux * 0.5f));
+      y = round_t<T>(to_f32(r[1]) + round_t<T>(uy * 0.5f));
     }
   }
 }

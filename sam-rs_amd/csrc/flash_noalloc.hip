@@ -22,9 +22,20 @@
 
 namespace samhip {
 int report_error(int code, const std::string& msg);  // sam_hip_abi.cpp: the message of sam_hip_last_error
-}
+// sam_hip_abi.cpp: the workspace query and the flash entry point with the key-split plan of at most
+// cu_cap CUs
+long flash_workspace_size_capped(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k, int cu_cap);
+int flash_attn_capped(const void* q, const void* k, const void* v, void* out, int dtype, int b, int lq, int lk, int h,
+                      int d, const long* strides_q, const long* strides_k, const long* strides_v,
+                      const long* strides_o, float scale, const float* rope_cos, const float* rope_sin, int rope_rows,
+                      int n_rope_q, int n_rope_k, void* workspace, long workspace_bytes, void* stream, int cu_cap);
+}  // namespace samhip
 
 constexpr long kScratchBytes = SAM_HIP_FLASH_NOALLOC_MAX_BYTES;  // 64 MiB
+// The key-split count grows with the CU count, and the partial results with it; planning as for at most
+// 256 CUs (an MI355X) makes a call's workspace need independent of the device, so a call that fits on
+// one device fits on all.
+constexpr int kPlanCUs = 256;
 
 static __device__ __attribute__((aligned(256))) unsigned char scratch[kScratchBytes];
 
@@ -62,11 +73,13 @@ extern "C" int sam_hip_flash_attn_noalloc(const void* q, const void* k, const vo
                                           const long* strides_v, const long* strides_o, float scale,
                                           const float* rope_cos, const float* rope_sin, int rope_rows, int n_rope_q,
                                           int n_rope_k, void* stream) {
-  // Size checks first (no device call): the same plan sam_hip_flash_attn uses.
-  const long need = sam_hip_flash_attn_workspace_size(dtype, b, lq, lk, h, d, n_rope_k);
-  if (need < 0) return sam_hip_flash_attn(q, k, v, out, dtype, b, lq, lk, h, d, strides_q, strides_k, strides_v,
-                                          strides_o, scale, rope_cos, rope_sin, rope_rows, n_rope_q, n_rope_k,
-                                          nullptr, 0, stream);  // reports the size error
+  // The switch and the size checks first (no device call): the plan of sam_hip_flash_attn on a device of
+  // at most kPlanCUs CUs.
+  const long need = samhip::flash_workspace_size_capped(dtype, b, lq, lk, h, d, n_rope_k, kPlanCUs);
+  if (!sam_hip_enabled() || need < 0)  // reports the switch or the size error
+    return samhip::flash_attn_capped(q, k, v, out, dtype, b, lq, lk, h, d, strides_q, strides_k, strides_v, strides_o,
+                                     scale, rope_cos, rope_sin, rope_rows, n_rope_q, n_rope_k, nullptr, 0, stream,
+                                     kPlanCUs);
   if (need > kScratchBytes) {
     char buf[256];
     snprintf(buf, sizeof buf,
@@ -81,7 +94,7 @@ extern "C" int sam_hip_flash_attn_noalloc(const void* q, const void* k, const vo
     ws = scratch_on_current_device(&why);
     if (!ws) return samhip::report_error(SAM_HIP_EHIP, "flash-attn-noalloc: " + why);
   }
-  return sam_hip_flash_attn(q, k, v, out, dtype, b, lq, lk, h, d, strides_q, strides_k, strides_v, strides_o, scale,
-                            rope_cos, rope_sin, rope_rows, n_rope_q, n_rope_k, ws, need > 0 ? kScratchBytes : 0,
-                            stream);
+  return samhip::flash_attn_capped(q, k, v, out, dtype, b, lq, lk, h, d, strides_q, strides_k, strides_v, strides_o,
+                                   scale, rope_cos, rope_sin, rope_rows, n_rope_q, n_rope_k, ws,
+                                   need > 0 ? kScratchBytes : 0, stream, kPlanCUs);
 }

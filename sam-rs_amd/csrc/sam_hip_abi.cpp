@@ -2,9 +2,11 @@
 // reference's error behaviour, dtype dispatch, and the kernel launches.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "../../include/sam_hip.h"
@@ -65,6 +67,24 @@ int check_launch(hipError_t e, const char* what) {
 // The reference's dtype dispatch (kernels.rs:1086-1095) accepts exactly f16, bf16 and f32.
 bool dtype_ok(int dtype) { return dtype == 0 || dtype == 1 || dtype == 2; }
 
+// The process-wide switch of sam_hip_set_enabled, the counterpart of the reference's cpu_gemm::ENABLED
+// (cpu_gemm.rs:11, 25-32): on unless the environment variable SAM_HIP_DISABLE is set to anything but
+// "" or "0" when the library is loaded; sam_hip_set_enabled changes it at any time.
+bool initially_enabled() {
+  const char* e = std::getenv("SAM_HIP_DISABLE");
+  return !(e && e[0] && !(e[0] == '0' && e[1] == 0));
+}
+std::atomic<bool> g_enabled{initially_enabled()};
+
+// Every compute entry point starts here: when the switch is off it returns SAM_HIP_EDISABLED before
+// looking at any argument, and no device call is made.
+#define SAM_HIP_REQUIRE_ENABLED(what)                                                                       \
+  do {                                                                                                      \
+    if (!g_enabled.load(std::memory_order_relaxed))                                                         \
+      return fail(SAM_HIP_EDISABLED, "%s: the HIP path is switched off (sam_hip_set_enabled(0) or "        \
+                  "SAM_HIP_DISABLE); take the reference path", what);                                       \
+  } while (0)
+
 // The kernels move their operands in 16-byte vectors (and by 16-byte LDS DMA), which the header's
 // alignment rule guarantees; a pointer that breaks it is rejected rather than read.
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -81,12 +101,17 @@ int report_error(int code, const std::string& msg) {
 
 extern "C" {
 
-int sam_hip_abi_version(void) { return 3; }
+int sam_hip_abi_version(void) { return 4; }
+
+void sam_hip_set_enabled(int on) { g_enabled.store(on != 0, std::memory_order_relaxed); }
+
+int sam_hip_enabled(void) { return g_enabled.load(std::memory_order_relaxed) ? 1 : 0; }
 
 const char* sam_hip_last_error(void) { return g_last_error.c_str(); }
 
 int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void* table, void* out, int dtype, int bh,
                         int h, int w, int hd, float scale, void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("attn-relpos");
   if (!q || !kt || !v || !table || !out) return fail(SAM_HIP_EINVAL, "attn-relpos: null pointer argument");
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (bh <= 0 || h <= 0 || w <= 0 || hd <= 0)
@@ -134,6 +159,7 @@ int check_deform(const void* value, const void* out, int dtype, int b, int s, in
 
 int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, void* out, int dtype, int b, int s,
                         int q, int h, int d, int l, int p, const int* shapes, void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("deform-attn");
   if (!value || !loc || !attn || !out || !shapes) return fail(SAM_HIP_EINVAL, "deform-attn: null pointer argument");
   if (int rc = check_deform(value, out, dtype, b, s, q, h, d, l, p, shapes); rc != SAM_HIP_OK) return rc;
   hipError_t e = samhip::deform_attn(dtype, value, loc, attn, out, b, s, q, h, d, l, p, shapes,
@@ -144,6 +170,7 @@ int sam_hip_deform_attn(const void* value, const void* loc, const void* attn, vo
 int sam_hip_deform_core(const void* value, const void* offsets, const void* logits, const void* refs, void* out,
                         int dtype, int b, int s, int q, int h, int d, int l, int p, int ncoord, const int* shapes,
                         void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("deform-core");
   if (!value || !offsets || !logits || !refs || !out || !shapes)
     return fail(SAM_HIP_EINVAL, "deform-core: null pointer argument");
   if (ncoord != 2 && ncoord != 4)
@@ -156,6 +183,7 @@ int sam_hip_deform_core(const void* value, const void* offsets, const void* logi
 
 int sam_hip_preprocess(const void* img, void* out, int dtype, int h, int w, int nh, int nw, int size,
                        const float* mean, const float* std_dev, void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("preprocess");
   if (!img || !out || !mean || !std_dev) return fail(SAM_HIP_EINVAL, "preprocess: null pointer argument");
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (h <= 0 || w <= 0 || size <= 0)
@@ -177,6 +205,7 @@ int sam_hip_preprocess(const void* img, void* out, int dtype, int h, int w, int 
 
 int sam_hip_bias_residual(const void* res, const void* y, const void* bias, void* out, int dtype, long total, int c,
                           void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("bias-residual");
   if (!res || !y || !bias || !out) return fail(SAM_HIP_EINVAL, "bias-residual: null pointer argument");
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (total < 0 || c <= 0 || total % c != 0)
@@ -187,6 +216,7 @@ int sam_hip_bias_residual(const void* res, const void* y, const void* bias, void
 
 int sam_hip_bias_residual_ln(const void* res, const void* y, const void* bias, const void* ln_w, const void* ln_b,
                              void* out, void* ln_out, int dtype, long rows, int c, float eps, void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("bias-residual-ln");
   if (!res || !y || !bias || !ln_w || !ln_b || !out || !ln_out)
     return fail(SAM_HIP_EINVAL, "bias-residual-ln: null pointer argument");
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
@@ -208,6 +238,7 @@ int sam_hip_bias_residual_ln(const void* res, const void* y, const void* bias, c
 }
 
 int sam_hip_bias_gelu(const void* y, const void* bias, void* out, int dtype, long total, int c, void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("bias-gelu");
   if (!y || !bias || !out) return fail(SAM_HIP_EINVAL, "bias-gelu: null pointer argument");
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (total < 0 || c <= 0 || total % c != 0)
@@ -218,6 +249,7 @@ int sam_hip_bias_gelu(const void* y, const void* bias, void* out, int dtype, lon
 
 int sam_hip_relpos_softmax(const void* s, const void* q, const void* table, void* out, int dtype, long rows, int h,
                            int w, int hd, float scale, void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("relpos-softmax");
   if (!s || !q || !table || !out) return fail(SAM_HIP_EINVAL, "relpos-softmax: null pointer argument");
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (rows <= 0 || h <= 0 || w <= 0 || hd <= 0)
@@ -239,12 +271,15 @@ int sam_hip_relpos_softmax(const void* s, const void* q, const void* table, void
 
 int sam_hip_qkv_split(const void* y, const void* bias, void* out, int dtype, long tokens, int n, int nh, int hd,
                       void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("qkv-split");
   if (!y || !bias || !out) return fail(SAM_HIP_EINVAL, "qkv-split: null pointer argument");
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (tokens <= 0 || n <= 0 || nh <= 0 || hd <= 0)
     return fail(SAM_HIP_EINVAL, "qkv-split: sizes must be positive (tokens=%ld n=%d nh=%d hd=%d)", tokens, n, nh, hd);
   if (tokens % n != 0) return fail(SAM_HIP_EINVAL, "qkv-split: %ld tokens is not a multiple of n = %d", tokens, n);
   if (hd > 256) return fail(SAM_HIP_EUNSUPPORTED, "qkv-split: head dim at most 256, got %d", hd);
+  if (3L * nh * hd > 0x7fffffffL)  // the kernel's row arithmetic (the 3*nh*hd columns of y) is 32-bit
+    return fail(SAM_HIP_EUNSUPPORTED, "qkv-split: 3*nh*hd = %ld columns is beyond 2^31", 3L * nh * hd);
   const long blocks = tokens / n * ((n + 63) / 64) * nh;
   if (blocks > 0x7fffffffL) return fail(SAM_HIP_EUNSUPPORTED, "qkv-split: too many tokens");
   if (!aligned16(y) || !aligned16(bias) || !aligned16(out))
@@ -255,6 +290,7 @@ int sam_hip_qkv_split(const void* y, const void* bias, void* out, int dtype, lon
 
 int sam_hip_qkv_split_grid(const void* y, const void* bias, void* out, int dtype, int batch, int gh, int gw, int ws,
                            int nh, int hd, void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("qkv-split-grid");
   if (!y || !bias || !out) return fail(SAM_HIP_EINVAL, "qkv-split-grid: null pointer argument");
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (batch <= 0 || gh <= 0 || gw <= 0 || ws <= 0 || nh <= 0 || hd <= 0)
@@ -266,6 +302,9 @@ int sam_hip_qkv_split_grid(const void* y, const void* bias, void* out, int dtype
   const long n = (long)ws * ws;
   if (windows * ((n + 63) / 64) * nh > 0x7fffffffL || windows * n * 3L * nh * hd >= (1L << 40))
     return fail(SAM_HIP_EUNSUPPORTED, "qkv-split-grid: too many tokens");
+  // the kernel's row arithmetic (the 3*nh*hd columns of y) is 32-bit
+  if (3L * nh * hd > 0x7fffffffL)
+    return fail(SAM_HIP_EUNSUPPORTED, "qkv-split-grid: 3*nh*hd = %ld columns is beyond 2^31", 3L * nh * hd);
   if (!aligned16(y) || !aligned16(bias) || !aligned16(out))
     return fail(SAM_HIP_EUNSUPPORTED, "qkv-split-grid: y, bias and out must be 16-byte aligned");
   hipError_t e =
@@ -275,6 +314,7 @@ int sam_hip_qkv_split_grid(const void* y, const void* bias, void* out, int dtype
 
 int sam_hip_window_merge(const void* ctx, void* out, int dtype, int batch, int gh, int gw, int ws, int nh, int hd,
                          void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("window-merge");
   if (!ctx || !out) return fail(SAM_HIP_EINVAL, "window-merge: null pointer argument");
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (batch <= 0 || gh <= 0 || gw <= 0 || ws <= 0 || nh <= 0 || hd <= 0)
@@ -285,6 +325,9 @@ int sam_hip_window_merge(const void* ctx, void* out, int dtype, int batch, int g
   const long windows = (long)batch * ((gh + ws - 1) / ws) * ((gw + ws - 1) / ws);
   if (windows * ws * ws * (long)nh * hd >= (1L << 38))
     return fail(SAM_HIP_EUNSUPPORTED, "window-merge: too many elements");
+  // the kernel's row arithmetic (nh*hd columns of out) is 32-bit
+  if ((long)nh * hd > 0x7fffffffL)
+    return fail(SAM_HIP_EUNSUPPORTED, "window-merge: nh*hd = %ld columns is beyond 2^31", (long)nh * hd);
   if (!aligned16(ctx) || !aligned16(out))
     return fail(SAM_HIP_EUNSUPPORTED, "window-merge: ctx and out must be 16-byte aligned");
   hipError_t e = samhip::window_merge(dtype, ctx, out, batch, gh, gw, ws, nh, hd, reinterpret_cast<hipStream_t>(stream));
@@ -334,9 +377,12 @@ size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Workspace: key-split partials, then (when keys are rotated) the rotated keys and room for the rotated
 // queries, both contiguous [b, l, h, d], then (head dim 256) V as transposed key tiles.
-FlashPlan plan_flash(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k) {
+// cu_cap > 0 plans as if the device had at most that many CUs (fewer key splits, a smaller workspace).
+FlashPlan plan_flash(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k, int cu_cap) {
   FlashPlan pl;
-  samhip::flash_plan(b, h, lq, lk, d, device_cus(), &pl.qblocks, &pl.nsplit, &pl.tps);
+  int cus = device_cus();
+  if (cu_cap > 0 && cus > cu_cap) cus = cu_cap;
+  samhip::flash_plan(b, h, lq, lk, d, cus, &pl.qblocks, &pl.nsplit, &pl.tps);
   pl.partial_bytes = round256(samhip::flash_partial_bytes(b, h, lq, d, pl.nsplit));
   const size_t elem = dtype == 0 ? 4 : 2;
   pl.krot_bytes = n_rope_k > 0 ? round256((size_t)b * lk * h * d * elem) : 0;
@@ -363,7 +409,7 @@ extern "C" {
 
 long sam_hip_flash_attn_workspace_size(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k) {
   if (check_flash_sizes(dtype, b, lq, lk, h, d) != SAM_HIP_OK) return -1;
-  return (long)plan_flash(dtype, b, lq, lk, h, d, n_rope_k).total;
+  return (long)plan_flash(dtype, b, lq, lk, h, d, n_rope_k, 0).total;
 }
 
 // sam_hip_flash_attn, and sam_hip_sdpa_mask when mask is not null (no RoPE then).
@@ -371,7 +417,8 @@ static int flash_entry(const void* q, const void* k, const void* v, void* out, i
                        int d, const long* strides_q, const long* strides_k, const long* strides_v,
                        const long* strides_o, float scale, const float* rope_cos, const float* rope_sin,
                        int rope_rows, int n_rope_q, int n_rope_k, void* workspace, long workspace_bytes,
-                       void* stream, const void* mask, const long* strides_mask) {
+                       void* stream, const void* mask, const long* strides_mask, int cu_cap) {
+  SAM_HIP_REQUIRE_ENABLED(mask ? "sdpa-mask" : "flash-attn");
   if (!q || !k || !v || !out) return fail(SAM_HIP_EINVAL, "flash-attn: null pointer argument");
   int rc = check_flash_sizes(dtype, b, lq, lk, h, d);
   if (rc != SAM_HIP_OK) return rc;
@@ -401,7 +448,7 @@ static int flash_entry(const void* q, const void* k, const void* v, void* out, i
       return fail(SAM_HIP_EUNSUPPORTED, "sdpa-mask: the mask must be aligned to its element size");
     p.mask = mask;
   }
-  const FlashPlan pl = plan_flash(dtype, b, lq, lk, h, d, n_rope_k);
+  const FlashPlan pl = plan_flash(dtype, b, lq, lk, h, d, n_rope_k, cu_cap);
   if (pl.total > 0 && (!workspace || workspace_bytes < (long)pl.total))
     return fail(SAM_HIP_EINVAL, "flash-attn: needs a workspace of %zu bytes (sam_hip_flash_attn_workspace_size), got %ld",
                 pl.total, workspace ? workspace_bytes : 0L);
@@ -476,20 +523,43 @@ int sam_hip_flash_attn(const void* q, const void* k, const void* v, void* out, i
                        void* stream) {
   return flash_entry(q, k, v, out, dtype, b, lq, lk, h, d, strides_q, strides_k, strides_v, strides_o, scale,
                      rope_cos, rope_sin, rope_rows, n_rope_q, n_rope_k, workspace, workspace_bytes, stream, nullptr,
-                     nullptr);
+                     nullptr, 0);
 }
 
 int sam_hip_sdpa_mask(const void* q, const void* k, const void* v, const void* mask, void* out, int dtype, int b,
                       int lq, int lk, int h, int d, const long* strides_q, const long* strides_k,
                       const long* strides_v, const long* strides_mask, const long* strides_o, float scale,
                       void* workspace, long workspace_bytes, void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("sdpa-mask");
   if (!mask) return fail(SAM_HIP_EINVAL, "sdpa-mask: null mask (use sam_hip_flash_attn for mask None)");
   return flash_entry(q, k, v, out, dtype, b, lq, lk, h, d, strides_q, strides_k, strides_v, strides_o, scale, nullptr,
-                     nullptr, 0, 0, 0, workspace, workspace_bytes, stream, mask, strides_mask);
+                     nullptr, 0, 0, 0, workspace, workspace_bytes, stream, mask, strides_mask, 0);
 }
+
+}  // extern "C"
+
+namespace samhip {
+// sam_hip_flash_attn_workspace_size and sam_hip_flash_attn with the key-split plan of a device of at
+// most cu_cap CUs (sam_hip_flash_attn_noalloc, whose workspace has a fixed size).
+long flash_workspace_size_capped(int dtype, int b, int lq, int lk, int h, int d, int n_rope_k, int cu_cap) {
+  if (check_flash_sizes(dtype, b, lq, lk, h, d) != SAM_HIP_OK) return -1;
+  return (long)plan_flash(dtype, b, lq, lk, h, d, n_rope_k, cu_cap).total;
+}
+int flash_attn_capped(const void* q, const void* k, const void* v, void* out, int dtype, int b, int lq, int lk, int h,
+                      int d, const long* strides_q, const long* strides_k, const long* strides_v,
+                      const long* strides_o, float scale, const float* rope_cos, const float* rope_sin, int rope_rows,
+                      int n_rope_q, int n_rope_k, void* workspace, long workspace_bytes, void* stream, int cu_cap) {
+  return flash_entry(q, k, v, out, dtype, b, lq, lk, h, d, strides_q, strides_k, strides_v, strides_o, scale,
+                     rope_cos, rope_sin, rope_rows, n_rope_q, n_rope_k, workspace, workspace_bytes, stream, nullptr,
+                     nullptr, cu_cap);
+}
+}  // namespace samhip
+
+extern "C" {
 
 int sam_hip_rope(const void* x, const float* cos_t, const float* sin_t, void* out, int dtype, int b, int l, int h,
                  int d, const long* strides_x, const long* strides_out, int rope_rows, int n_rot, void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("rope");
   if (!x || !cos_t || !sin_t || !out) return fail(SAM_HIP_EINVAL, "rope: null pointer argument");
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (b <= 0 || l <= 0 || h <= 0 || d <= 0 || rope_rows <= 0)

@@ -13,8 +13,11 @@ Names, argument meaning and errors follow the reference:
     sdpa(q, k, v, mask=None)                             sam3/nn.rs:26-34
     rope(x, cos, sin)                                    sam3/video.rs:106-113
     rope_attention(q, k, v, cos, sin, n_exclude)         sam3/video.rs:129-145 (after the projections)
+    set_enabled(on), enabled()                           cpu_gemm.rs:11, 25-32 (the process-wide switch)
 
-There is no CPU fallback: on a machine without the built library or a GPU every call raises.
+There is no CPU fallback: on a machine without the built library or a GPU every call raises. While the
+switch is off every call raises SamHipDisabled without touching the device; the caller then takes its
+own path, as the reference's callers do when cpu_gemm::enabled() is false.
 """
 from __future__ import annotations
 
@@ -35,6 +38,13 @@ _f = ctypes.c_float
 
 class SamHipError(RuntimeError):
     """An error reported by libsam_hip.so (the message is the library's own)."""
+
+
+class SamHipDisabled(SamHipError):
+    """The HIP path is switched off (set_enabled(False) or SAM_HIP_DISABLE); nothing was done."""
+
+
+_EDISABLED = 5  # SAM_HIP_EDISABLED
 
 
 def load():
@@ -81,13 +91,28 @@ def load():
         L.sam_hip_rope.restype = _i
         L.sam_hip_sdpa_mask.argtypes = [_vp] * 5 + [_i] * 6 + [_lp] * 5 + [_f, _vp, ctypes.c_long, _vp]
         L.sam_hip_sdpa_mask.restype = _i
+        L.sam_hip_set_enabled.argtypes = [_i]
+        L.sam_hip_set_enabled.restype = None
+        L.sam_hip_enabled.argtypes = []
+        L.sam_hip_enabled.restype = _i
         _lib = L
     return _lib
 
 
 def _check(rc: int):
     if rc != 0:
-        raise SamHipError(load().sam_hip_last_error().decode())
+        msg = load().sam_hip_last_error().decode()
+        raise (SamHipDisabled if rc == _EDISABLED else SamHipError)(msg)
+
+
+def set_enabled(on: bool) -> None:
+    """Turn the HIP path on or off for the whole process (cpu_gemm::set_enabled, cpu_gemm.rs:25-28)."""
+    load().sam_hip_set_enabled(1 if on else 0)
+
+
+def enabled() -> bool:
+    """Whether the HIP path is on (cpu_gemm::enabled, cpu_gemm.rs:30-32)."""
+    return bool(load().sam_hip_enabled())
 
 
 def _stream():
@@ -367,7 +392,11 @@ def _strides_blhd(t: torch.Tensor, layout: str):
 
 def _flash(q, k, v, out, layout: str, scale: float, cos=None, sin=None, n_rope_q: int = 0, n_rope_k: int = 0,
            noalloc: bool = False):
-    for t in (q, k, v):
+    # the kernel writes q.shape elements of q's dtype through out's pointer: anything else is refused
+    if out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
+        raise SamHipError(f"flash-attn: out must match q (shape {tuple(q.shape)}, {q.dtype}, {q.device}), got "
+                          f"{tuple(out.shape)}, {out.dtype}, {out.device}")
+    for t in (q, k, v, out):
         if not t.is_cuda:
             raise SamHipError("sam-rs HIP kernels need device tensors")
     dt = _dtype(q, k, v)

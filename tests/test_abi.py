@@ -5,6 +5,7 @@ import os
 import re
 
 import pytest
+import torch
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "sam_hip.h")
@@ -99,6 +100,103 @@ def test_flash_and_rope_argument_checks(lib):
     lib.sam_hip_rope.argtypes = [vp] * 4 + [i] * 5 + [lp] * 2 + [i, i, vp]
     assert lib.sam_hip_rope(fake, fake, fake, fake, 1, 1, 8, 1, 12, None, None, 8, 8, None) == 3
     assert lib.sam_hip_rope(fake, fake, fake, fake, 1, 1, 8, 1, 16, None, None, 8, 9, None) == 1
+
+
+def test_column_counts_beyond_int_are_refused(lib):
+    """qkv_split, qkv_split_grid and window_merge index rows of nh*hd (or 3*nh*hd) columns in 32-bit
+    arithmetic: a head count that overflows it is refused, even where the total element count passes."""
+    lib.sam_hip_last_error.restype = ctypes.c_char_p
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    fake = vp(0x1000)
+    lib.sam_hip_qkv_split.argtypes = [vp] * 3 + [i, ctypes.c_long, i, i, i, vp]
+    lib.sam_hip_qkv_split_grid.argtypes = [vp] * 3 + [i] * 7 + [vp]
+    lib.sam_hip_window_merge.argtypes = [vp] * 2 + [i] * 7 + [vp]
+    nh = (1 << 31) // (3 * 8) + 1  # 3 * nh * 8 just past 2^31; one token, one 1x1 window
+    assert lib.sam_hip_qkv_split(fake, fake, fake, 1, 1, 1, nh, 8, None) == 3
+    assert b"3*nh*hd" in lib.sam_hip_last_error()
+    assert lib.sam_hip_qkv_split_grid(fake, fake, fake, 1, 1, 1, 1, 1, nh, 8, None) == 3
+    assert b"3*nh*hd" in lib.sam_hip_last_error()
+    nh2 = (1 << 31) // 8 + 1  # nh * 8 just past 2^31, 2^31 + 8 elements in total
+    assert lib.sam_hip_window_merge(fake, fake, 1, 1, 1, 1, 1, nh2, 8, None) == 3
+
+
+def test_the_switch_turns_every_entry_point_off_and_on(lib):
+    """sam_hip_set_enabled mirrors cpu_gemm::set_enabled (cpu_gemm.rs:25-32): while it is off, every
+    compute entry point returns SAM_HIP_EDISABLED (5) before reading its arguments (null pointers and
+    impossible sizes included, so nothing reaches a device); once it is on again, the ordinary argument
+    checks answer."""
+    lib.sam_hip_last_error.restype = ctypes.c_char_p
+    lib.sam_hip_enabled.restype = ctypes.c_int
+    lib.sam_hip_set_enabled.argtypes = [ctypes.c_int]
+    vp, i, f, lp = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.POINTER(ctypes.c_long)
+    sigs = {
+        "sam_hip_attn_relpos": [vp] * 5 + [i] * 5 + [f, vp],
+        "sam_hip_relpos_softmax": [vp] * 4 + [i, ctypes.c_long, i, i, i, f, vp],
+        "sam_hip_qkv_split": [vp] * 3 + [i, ctypes.c_long, i, i, i, vp],
+        "sam_hip_qkv_split_grid": [vp] * 3 + [i] * 7 + [vp],
+        "sam_hip_window_merge": [vp] * 2 + [i] * 7 + [vp],
+        "sam_hip_deform_attn": [vp] * 4 + [i] * 8 + [vp, vp],
+        "sam_hip_deform_core": [vp] * 5 + [i] * 9 + [vp, vp],
+        "sam_hip_preprocess": [vp, vp] + [i] * 6 + [vp, vp, vp],
+        "sam_hip_bias_residual": [vp] * 4 + [i, ctypes.c_long, i, vp],
+        "sam_hip_bias_gelu": [vp] * 3 + [i, ctypes.c_long, i, vp],
+        "sam_hip_bias_residual_ln": [vp] * 7 + [i, ctypes.c_long, i, f, vp],
+        "sam_hip_flash_attn": [vp] * 4 + [i] * 6 + [lp] * 4 + [f, vp, vp, i, i, i, vp, ctypes.c_long, vp],
+        "sam_hip_flash_attn_noalloc": [vp] * 4 + [i] * 6 + [lp] * 4 + [f, vp, vp, i, i, i, vp],
+        "sam_hip_sdpa_mask": [vp] * 5 + [i] * 6 + [lp] * 5 + [f, vp, ctypes.c_long, vp],
+        "sam_hip_rope": [vp] * 4 + [i] * 5 + [lp] * 2 + [i, i, vp],
+    }
+    # every declared compute entry point is covered
+    queries = {"sam_hip_flash_attn_workspace_size", "sam_hip_last_error", "sam_hip_abi_version",
+               "sam_hip_set_enabled", "sam_hip_enabled"}
+    assert set(declared_functions()) - queries == set(sigs)
+
+    def zeros(argtypes):  # null pointers and zero sizes: every call is invalid as an ordinary call
+        return [None if t in (vp, lp) else (0.0 if t is f else 0) for t in argtypes]
+
+    assert lib.sam_hip_enabled() == 1
+    try:
+        lib.sam_hip_set_enabled(0)
+        assert lib.sam_hip_enabled() == 0
+        for name, argtypes in sigs.items():
+            fn = getattr(lib, name)
+            fn.argtypes, fn.restype = argtypes, ctypes.c_int
+            assert fn(*zeros(argtypes)) == 5, name
+            assert b"switched off" in lib.sam_hip_last_error(), name
+    finally:
+        lib.sam_hip_set_enabled(1)
+    assert lib.sam_hip_enabled() == 1
+    for name, argtypes in sigs.items():
+        rc = getattr(lib, name)(*zeros(argtypes))
+        assert rc in (1, 2, 3), (name, rc)  # EINVAL, EDTYPE or EUNSUPPORTED: argument checks, no launch
+
+
+def test_the_switch_reads_sam_hip_disable_at_load_time():
+    """SAM_HIP_DISABLE=1 in the environment starts the library switched off (a fresh process, so that
+    this process's library state is untouched)."""
+    if not os.path.exists(LIB):
+        pytest.skip("libsam_hip.so is not built")
+    import subprocess
+    import sys
+
+    code = ("import ctypes, sys; L = ctypes.CDLL(sys.argv[1]); L.sam_hip_enabled.restype = ctypes.c_int; "
+            "print(L.sam_hip_enabled())")
+    for env_value, want in (("1", "0"), ("0", "1"), ("", "1")):
+        env = dict(os.environ, SAM_HIP_DISABLE=env_value)
+        out = subprocess.run([sys.executable, "-c", code, LIB], env=env, capture_output=True, text=True, check=True)
+        assert out.stdout.strip() == want, (env_value, out.stdout, out.stderr)
+
+
+def test_python_flash_refuses_a_mismatched_out():
+    """flash_attn writes q.shape elements of q's dtype through `out`: a smaller, narrower or
+    differently placed `out` is refused before any library call (CPU tensors suffice)."""
+    import sam_hip
+
+    q = torch.zeros(1, 8, 2, 16, dtype=torch.float16)
+    for bad in (torch.zeros(1, 4, 2, 16, dtype=torch.float16), torch.zeros(1, 8, 2, 16, dtype=torch.float32),
+                torch.zeros(1, 8, 2, 16, dtype=torch.float16, device="meta")):
+        with pytest.raises(sam_hip.SamHipError, match="out must match q"):
+            sam_hip.flash_attn(q, q, q, out=bad)
 
 
 def test_abi_version(lib):

@@ -5,7 +5,8 @@ sam_hip_deform_core is the part of Deform::forward between its projections (dino
 softmax of the attention logits over a head's L*P points, the sampling locations from the offsets and
 the reference points, encoder form ref + off / (W, H) (2 coordinates) and decoder form
 xy + off / P * wh * 0.5 (4 coordinates), and the bilinear gather. The oracle runs its restatement
-(oracle_deform_prep, then oracle_deform_attn) on the same inputs, pre-rounded to the kernel dtype.
+(oracle_deform_prep, then oracle_deform_attn) on the same inputs, pre-rounded to the kernel dtype; for
+f16 / bf16 the restatement rounds each step to that dtype, as the reference's candle ops do.
 Bars: f32 max|gpu - cpu| / max|cpu| <= 1e-5; f16 max-abs 2e-3; bf16 2e-3 beyond its output rounding.
 """
 import numpy as np
@@ -68,7 +69,7 @@ CASES = [
 def test_deform_core_matches_oracle(hip, name, shapes, b, q, h, d, p, nc, dtype):
     print(f"deform core {name} nc={nc} {dtype}", flush=True)
     arrays = core_inputs(shapes, b, q, h, d, p, nc, 60 + q + nc, dtype)
-    want = oracle.deform_forward_core(*arrays, shapes)
+    want = oracle.deform_forward_core(*arrays, shapes, dtype=dtype)
     got = run_core(hip, arrays, shapes, dtype)
     check(got, want, dtype, f"deform core {name} nc={nc} {dtype}")
 
@@ -86,7 +87,7 @@ def test_deform_core_dino_tiny(hip, q, nc, dtype):
     if nc == 2:
         refs = sam_dino.encoder_reference_points(DINO_LEVELS, device="cpu").numpy()[None]
         arrays[3] = oracle.round_to(refs, dtype)
-    want = oracle.deform_forward_core(*arrays, DINO_LEVELS)
+    want = oracle.deform_forward_core(*arrays, DINO_LEVELS, dtype=dtype)
     got = run_core(hip, arrays, DINO_LEVELS, dtype)
     check(got, want, dtype, f"deform core dino-tiny q={q} {dtype}")
 

@@ -3,19 +3,20 @@
 Cases: the reference's own test shapes (tests/kernels.rs:65-83, tests/dino.rs:46-63) with sampling
 locations spread beyond [0, 1] so the zero padding is exercised, shapes that take each of the two
 kernels (16-byte lanes when D allows, scalar lanes otherwise) and multi-batch grids of hundreds of
-workgroups, plus the Grounding DINO-tiny encoder and decoder layers at full size. Bars: f32 max-abs 1e-4 (the reference test's, tests/kernels.rs:78); f16
-and bf16 max-abs against the f32 oracle on the same rounded inputs: 2e-3 (f16) and the reference
-test's 5e-2 (bf16, whose 8-bit inputs and output cannot do better on values ~N(0,1)).
+workgroups, plus the Grounding DINO-tiny encoder and decoder layers at full size. Bars (tests/parity.py,
+the attention bars): f32 max|gpu - cpu| / max|cpu| <= 1e-5; f16 max-abs 2e-3 and bf16 max-abs 2e-3
+beyond the output's own rounding, against the f32 oracle on the same rounded inputs. These are tighter
+than the reference test's own (f32 1e-4, bf16 5e-2; tests/kernels.rs:65-83).
 """
 import numpy as np
 import pytest
 import torch
 
 import sam_oracle as oracle
+from parity import check
 
 pytestmark = pytest.mark.gpu
 TORCH_DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
-TOL = {"f32": 1e-4, "f16": 2e-3, "bf16": 5e-2}
 
 DINO_LEVELS = [(100, 167), (50, 84), (25, 42), (13, 21)]
 
@@ -67,14 +68,14 @@ def test_deform_matches_oracle(hip, name, shapes, b, q, h, d, p, spread, dtype):
     arrays = inputs(shapes, b, q, h, d, p, 20 + q, spread, dtype)
     want = oracle.deform_attn(*arrays, shapes)
     got = run(hip, arrays, shapes, dtype)
-    err = np.abs(got - want).max()
-    assert np.isfinite(got).all() and err <= TOL[dtype], f"{name} {dtype}: max abs diff {err:.3g}"
+    check(got, want, dtype, f"deform {name} {dtype}")
 
 
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("q", [22223, 900], ids=["encoder", "decoder"])
-def test_dino_tiny_full_size(hip, q):
+def test_dino_tiny_full_size(hip, q, dtype):
     """Grounding DINO-tiny: 800x1333 input -> 4 levels, 22223 value tokens, 8 heads x 32, 4 points."""
-    print(f"deform dino-tiny q={q}", flush=True)
+    print(f"deform dino-tiny q={q} {dtype}", flush=True)
     r = np.random.default_rng(q)
     s = sum(a * b for a, b in DINO_LEVELS)
     value = r.standard_normal((1, s, 8, 32)).astype(np.float32)
@@ -84,9 +85,10 @@ def test_dino_tiny_full_size(hip, q):
     logits = r.standard_normal((1, q, 8, 16))
     attn = np.exp(logits - logits.max(-1, keepdims=True))
     attn = (attn / attn.sum(-1, keepdims=True)).reshape(1, q, 8, 4, 4).astype(np.float32)
+    value, loc, attn = (oracle.round_to(x, dtype) for x in (value, loc, attn))
     want = oracle.deform_attn(value, loc, attn, DINO_LEVELS)
-    got = run(hip, [value, loc, attn], DINO_LEVELS, "f32")
-    assert np.abs(got - want).max() <= 1e-4
+    got = run(hip, [value, loc, attn], DINO_LEVELS, dtype)
+    check(got, want, dtype, f"deform dino-tiny q={q} {dtype}")
 
 
 def test_pixel_centres_are_exact_gathers(hip):

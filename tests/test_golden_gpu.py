@@ -50,11 +50,7 @@ def test_deform_golden(hip, name, dtype):
     g = golden_io.load("deform", name)
     out = hip.deform_attn(to_dev(g["value"], dtype), to_dev(g["loc"], dtype), to_dev(g["attn"], dtype),
                           [tuple(x) for x in g["shapes"].tolist()])
-    got = host(out)
-    if dtype == "f32":
-        assert np.abs(got - g["out"]).max() <= 1e-4  # the reference's f32 bar (tests/kernels.rs:78)
-    else:
-        check(got, g["out"], dtype, f"deform golden {name} {dtype}")
+    check(host(out), g["out"], dtype, f"deform golden {name} {dtype}")
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])

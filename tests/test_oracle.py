@@ -245,6 +245,43 @@ def test_deform_prep_closed_forms(oracle_lib):
     assert np.array_equal(loc, np.broadcast_to(xy + wh, loc.shape))
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("nc", [2, 4])
+def test_deform_prep_rounds_each_step_to_the_dtype(oracle_lib, dtype, nc):
+    """With a 16-bit query, each candle op of dino/mod.rs:166-178 returns that dtype. The oracle's
+    rounded restatement equals the same steps run as torch CPU tensor ops in that dtype (each
+    elementwise op computed in f32 and rounded once; the softmax in f32, rounded at the end): the
+    locations bit for bit, the weights to one unit in the last place (the two softmaxes sum in
+    different orders). At DINO's 167-wide level the rounding moves sampling points far beyond the
+    2e-3 bar, so a restatement that skipped it would not pass as the reference."""
+    import torch
+
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16}[dtype]
+    shapes = [(100, 167), (50, 84), (25, 42), (13, 21)]
+    b, q, h, p = 1, 50, 8, 4
+    off, logits, refs = (oracle_lib.round_to(x, dtype) for x in _prep_inputs(shapes, b, q, h, p, nc, 77 + nc))
+    off[..., 0] *= 2.0  # offsets of a few pixels at the larger levels
+    off = oracle_lib.round_to(off, dtype)
+    loc, attn = oracle_lib.deform_prep(off, logits, refs, shapes, dtype=dtype)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(tdt)
+    o, r = t(off), t(refs)
+    if nc == 2:
+        norm = t(np.array([[ww, hh] for hh, ww in shapes], np.float32)).reshape(1, 1, 1, len(shapes), 1, 2)
+        want = r[:, :, None, :, None, :] + o / norm
+    else:
+        rr = r[:, :, None, :, None, :]
+        want = rr[..., :2] + ((o * (1.0 / p)) * rr[..., 2:]) * 0.5
+    assert want.dtype == tdt
+    assert np.array_equal(loc, want.float().numpy())
+    aw = torch.softmax(t(logits).float().reshape(b, q, h, -1), -1).to(tdt).float().numpy().reshape(attn.shape)
+    ulp = {"f16": 2.0 ** -10, "bf16": 2.0 ** -7}[dtype] * np.maximum(np.abs(aw), 2.0 ** -14)
+    assert (np.abs(attn - aw) <= ulp).all()
+    # the rounding matters: the f32 restatement of the same rounded inputs lies far from it
+    loc32, _ = oracle_lib.deform_prep(off, logits, refs, shapes)
+    px = np.abs(loc - loc32)[:, :, :, 0, :, 0].max() * 167  # in pixels of the 167-wide level
+    assert px > 2e-3
+
+
 def test_deform_prep_rejects_a_swapped_normaliser(oracle_lib):
     """A planted mistake, (H, W) in place of (W, H), is caught by the float64 module on non-square
     levels."""
