@@ -320,6 +320,33 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
         res[f"vit_h_{name}_layer_bf16"] = leg
         del qb, ktb, vb, ob
 
+    # Platform references for the MFMA roofline, on this GPU in this run: torch's own flash attention
+    # (scaled_dot_product_attention, no bias) at the ViT-H global layer's shape, and a plain hipBLASLt f16
+    # GEMM through torch. Neither is part of the path; they show what the platform's own kernels reach
+    # against the same 2516.6 TFLOP/s peak.
+    import torch.nn.functional as F
+
+    qs, ks, vs = (torch.randn(1, HEADS, 4096, HD, device=dev, generator=g).half() for _ in range(3))
+    try:
+        with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.FLASH_ATTENTION):
+            ms = timer.avg_ms(lambda: F.scaled_dot_product_attention(qs, ks, vs), 30, warm_s=0.1)
+        f = flops(HEADS, 4096)
+        res["reference_torch_flash_sdpa_vit_h_global_f16"] = {
+            "workload": f"torch scaled_dot_product_attention (flash backend, no rel-pos bias), [1, {HEADS}, 4096, {HD}] f16",
+            "us": round(ms * 1e3, 2), "tflops": round(f / (ms * 1e-3) / 1e12, 1),
+            "frac_of_f16_mfma_peak": round(f / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f16"], 4)}
+    except RuntimeError as e:  # no flash backend in this torch build
+        res["reference_torch_flash_sdpa_vit_h_global_f16"] = {"error": str(e)[:120]}
+    del qs, ks, vs
+    ga = torch.randn(8192, 8192, device=dev, generator=g).half()
+    gb = torch.randn(8192, 8192, device=dev, generator=g).half()
+    ms = timer.avg_ms(lambda: torch.matmul(ga, gb), 20, warm_s=0.1)
+    res["reference_hipblaslt_gemm_f16_8192"] = {
+        "workload": "torch.matmul f16 8192 x 8192 x 8192 (hipBLASLt)",
+        "us": round(ms * 1e3, 2), "tflops": round(2 * 8192 ** 3 / (ms * 1e-3) / 1e12, 1),
+        "frac_of_f16_mfma_peak": round(2 * 8192 ** 3 / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f16"], 4)}
+    del ga, gb
+
     # Grounding DINO-tiny deformable attention, f32: 4 levels of an 800x1333 input, 8 heads x 32, 4 points.
     shapes = [(100, 167), (50, 84), (25, 42), (13, 21)]
     s = sum(a * b for a, b in shapes)
@@ -621,7 +648,8 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
             res[f"vit_b_{name}_f32"]["cpu_baseline"] = cpu_leg(
                 tcpu, 1, 1e6, "us", "the whole layer on the reference's exact-f32 TiledAttention branch "
                                     "(kernels.rs:181-220), best of 2")
-    late = [k for k in ("dino_deform_core_decoder_f32", "dino_deform_decoder_f32", "dino_deform_core_encoder_f32",
+    late = [k for k in ("reference_hipblaslt_gemm_f16_8192", "reference_torch_flash_sdpa_vit_h_global_f16",
+                        "dino_deform_core_decoder_f32", "dino_deform_decoder_f32", "dino_deform_core_encoder_f32",
                         "dino_deform_encoder_f32", "sam2_memory_attention_f16", "vit_h_window_layer_bf16",
                         "vit_h_global_layer_bf16") if k in res]
     return {**{k: v for k, v in res.items() if k not in late}, **{k: res[k] for k in late}}
