@@ -351,6 +351,25 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
     shapes = [(100, 167), (50, 84), (25, 42), (13, 21)]
     s = sum(a * b for a, b in shapes)
     hh, dd, ll, pp = 8, 32, 4, 4
+    # The gather's own ceiling: 16-byte pieces of random 128-byte rows from one head's value rows (an
+    # L2-resident 2.85 MB region), 16 loads in flight per lane, as the deform gather reads its corner rows
+    # (measurement kernel in libsam_probe.so). Bytes delivered to registers / time.
+    probe = ctypes.CDLL(os.path.join(ROOT, "sam-rs_amd", "libsam_probe.so"))
+    probe.sam_probe_gather.argtypes = [vp, ctypes.c_uint, ctypes.c_int, ctypes.c_int, vp, vp]
+    region = torch.randn(s * dd, device=dev, generator=g)  # s rows of 128 bytes
+    pblocks, psteps = 1024, 256
+    pout = torch.empty(pblocks * 256, device=dev)
+    def run_probe():
+        if probe.sam_probe_gather(region.data_ptr(), s, psteps, pblocks, pout.data_ptr(), sp) != 0:
+            raise RuntimeError("gather probe launch failed")
+
+    pms = timer.avg_ms(run_probe, 20)
+    gather_ceiling_gbs = pblocks * 256 * psteps * 16 / (pms * 1e-3) / 1e9
+    res["gather_ceiling_16b_rows_l2"] = {
+        "workload": "16-byte loads of random 128-byte rows of a 2.85 MB region (one DINO-tiny head's value rows), "
+                    "8 lanes per row, 16 loads in flight per lane, 1024 x 256 lanes",
+        "us": round(pms * 1e3, 2), "gbs": round(gather_ceiling_gbs, 1)}
+    del region, pout
     value = torch.randn(1, s, hh, dd, device=dev, generator=g)
     flat = (ctypes.c_int * 8)(*[x for hw in shapes for x in hw])
     for name, q in (("encoder", s), ("decoder", 900)):
@@ -377,6 +396,7 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             # the corner rows the gather delivers to registers (4 per point, D f32 each)
             "gathered_bytes": gathered, "gathered_gbs": round(gathered / (ms * 1e-3) / 1e9, 1),
+            "frac_of_gather_ceiling": round(gathered / (ms * 1e-3) / 1e9 / gather_ceiling_gbs, 4),
         }
         if cpu:
             vh, lh, ah = host(value), host(loc), host(attn_w)
@@ -406,6 +426,7 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "gathered_bytes": gathered, "gathered_gbs": round(gathered / (ms * 1e-3) / 1e9, 1),
+            "frac_of_gather_ceiling": round(gathered / (ms * 1e-3) / 1e9 / gather_ceiling_gbs, 4),
         }
         if cpu:
             oh, gh, rh = host(off), host(logits), host(refs)

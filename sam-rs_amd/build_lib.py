@@ -1,9 +1,11 @@
 """Builds libsam_hip.so (the gfx950 kernels and their C ABI) in-tree with hipcc.
 
-    python sam-rs_amd/build_lib.py          # compile every source, link the library
+    python sam-rs_amd/build_lib.py          # compile every source, link the libraries
 
 Each source compiles to its own object in parallel (the attention kernels have many template
-instantiations), then everything links into sam-rs_amd/libsam_hip.so.
+instantiations), then everything links into sam-rs_amd/libsam_hip.so. The measurement kernel that
+bench.py uses for the gather ceiling (gather_probe.hip) links into sam-rs_amd/libsam_probe.so, apart
+from the product library.
 """
 from __future__ import annotations
 
@@ -17,6 +19,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsam_hip.so")
+PROBE_LIB = os.path.join(HERE, "libsam_probe.so")
+PROBE_SOURCES = ["gather_probe.hip"]
 
 SOURCES = [
     "attn_relpos.hip",
@@ -51,14 +55,20 @@ def _compile(src: str) -> str:
     return obj
 
 
+def _link(objs, lib: str) -> None:
+    tmp = lib + ".tmp"
+    subprocess.run([HIPCC, ARCH, "-shared", "-fPIC", "-o", tmp, *objs], check=True)
+    shutil.move(tmp, lib)
+
+
 def build(jobs: int | None = None) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
+    srcs = SOURCES + PROBE_SOURCES
+    jobs = jobs or min(len(srcs), os.cpu_count() or 1)
     with concurrent.futures.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
-    subprocess.run([HIPCC, ARCH, "-shared", "-fPIC", "-o", tmp, *objs], check=True)
-    shutil.move(tmp, LIB)
+        objs = list(ex.map(_compile, srcs))
+    _link(objs[:len(SOURCES)], LIB)
+    _link(objs[len(SOURCES):], PROBE_LIB)
     return LIB
 
 

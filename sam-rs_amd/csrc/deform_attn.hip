@@ -202,6 +202,25 @@ __global__ __launch_bounds__(kDeformThreads) void deform_attn_kernel(const T* __
 constexpr int kDeformUnroll = 16;
 constexpr unsigned kDeformSkip = 0xF0000000u;
 
+// Location and weight of a point from its staged inputs (the arithmetic of point_xyw, NC = 2 or 4):
+// lg = the point's exp(logit - max) (the softmax numerator), r = its reference point.
+template <typename T, int NC>
+__device__ __forceinline__ void staged_xyw(const float* st, float inv_p, float sum, int Wl, int Hl, float& x,
+                                           float& y, float& w) {
+#pragma clang fp contract(off)
+  const float e = st[0], ax = st[1], ay = st[2];
+  w = round_t<T>(e / sum);
+  if constexpr (NC == 2) {
+    x = round_t<T>(st[3] + round_t<T>(ax / round_t<T>((float)Wl)));
+    y = round_t<T>(st[4] + round_t<T>(ay / round_t<T>((float)Hl)));
+  } else {
+    const float ux = round_t<T>(round_t<T>(ax * inv_p) * st[5]);
+    const float uy = round_t<T>(round_t<T>(ay * inv_p) * st[6]);
+    x = round_t<T>(st[3] + round_t<T>(ux * 0.5f));
+    y = round_t<T>(st[4] + round_t<T>(uy * 0.5f));
+  }
+}
+
 template <typename T, int VEC, int NC>
 __global__ __launch_bounds__(kDeformThreads) void deform_attn_gather_kernel(const T* __restrict__ value,
                                                                            PointSrc<T> src,
@@ -230,7 +249,40 @@ __global__ __launch_bounds__(kDeformThreads) void deform_attn_gather_kernel(cons
   // corner table of this pair: ntab entries of (byte offset into value, weight)
   int2* corners = reinterpret_cast<int2*>(smem) + ((long)wave * ppw + sub) * ntab;
   float mx = 0.f, sum = 1.f;
-  if constexpr (NC != 0) pair_softmax(src.attn, pair * npt, npt, li, LP, valid, mx, sum);
+  if constexpr (NC != 0) {
+    // Deform::forward's inputs: every global load of the pair's points (logit, offsets, reference point)
+    // is issued in one pass and staged in the point's own 32 bytes of the corner table (this lane alone
+    // reads them back), then the softmax statistics, each exponential computed once.
+    float m = -INFINITY;
+#pragma unroll 2
+    for (int j = li; j < npt; j += LP) {
+      if (valid) {
+        const long base = pair * npt + j;
+        const T* r = src.refs + (bq * L + j / P) * NC;
+        float* st = reinterpret_cast<float*>(corners + j * 4);
+        const float lg = to_f32(src.attn[base]);
+        st[0] = lg;
+        st[1] = to_f32(src.loc[base * 2]);
+        st[2] = to_f32(src.loc[base * 2 + 1]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) st[3 + c] = to_f32(r[c]);
+        m = fmaxf(m, lg);
+      }
+    }
+    for (int o = LP >> 1; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    float ssum = 0.f;
+    for (int j = li; j < npt; j += LP) {
+      if (valid) {
+        float* st = reinterpret_cast<float*>(corners + j * 4);
+        const float e = expf(st[0] - m);
+        st[0] = e;
+        ssum += e;
+      }
+    }
+    for (int o = LP >> 1; o > 0; o >>= 1) ssum += __shfl_xor(ssum, o);
+    mx = m;
+    sum = ssum;
+  }
   for (int j = li; j < (ntab >> 2); j += LP) {
     int2 c4[4];
 #pragma unroll
@@ -240,7 +292,14 @@ __global__ __launch_bounds__(kDeformThreads) void deform_attn_gather_kernel(cons
       // point ((b*Q + q)*H + h)*L*P + l*P + p
       const int Hl = lv.h[l], Wl = lv.w[l];
       float lx, ly, wgt;
-      point_xyw<T, NC>(src, pair, bq, npt, j, l, L, Wl, Hl, mx, sum, lx, ly, wgt);
+      if constexpr (NC != 0) {
+        float st[3 + NC];
+#pragma unroll
+        for (int c = 0; c < 3 + NC; ++c) st[c] = reinterpret_cast<const float*>(corners + j * 4)[c];
+        staged_xyw<T, NC>(st, src.inv_p, sum, Wl, Hl, lx, ly, wgt);
+      } else {
+        point_xyw<T, NC>(src, pair, bq, npt, j, l, L, Wl, Hl, mx, sum, lx, ly, wgt);
+      }
       const float x = lx * (float)Wl - 0.5f;
       const float y = ly * (float)Hl - 0.5f;
       const float xf = floorf(x), yf = floorf(y);
