@@ -540,8 +540,8 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
             }
         if cpu:
             # the reference's default CPU attention (bf16 branch on AVX-512 BF16 hosts, else exact f32) per
-            # image: 5 of the 25 windows and 2 of the heads of a global layer, scaled up (the CPU cost is
-            # linear in units and in batch)
+            # image: one whole windowed layer (25 windows x heads) and one whole global layer, scaled by the
+            # encoder's layer counts (the CPU cost is linear in layers and in batch)
             fn = orc.bf16_attention_relpos if orc.bf16_available() else orc.attention_relpos
             rr = np.random.default_rng(3)
 
@@ -552,14 +552,15 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
                         rr.standard_normal((bh, n, hd), dtype=np.float32),
                         (0.02 * rr.standard_normal((4 * side - 2, hd))).astype(np.float32))
 
-            wu, gu = units(5 * heads, 14), units(2, 64)
+            wu, gu = units(WINDOWS * heads, 14), units(heads, 64)
             tw = best_of(lambda: fn(*wu, 14, 14, hd ** -0.5, nthreads=cores), 2)
             tg = best_of(lambda: fn(*gu, 64, 64, hd ** -0.5, nthreads=cores), 2)
             ng_ = len(glob)
-            leg = cpu_leg(1.0, 1.0, 1e3 * ((depth - ng_) * tw * 5 + ng_ * tg * heads / 2), "ms/image",
+            leg = cpu_leg(1.0, 1.0, 1e3 * ((depth - ng_) * tw + ng_ * tg), "ms/image",
                           f"{'bf16' if orc.bf16_available() else 'exact f32'} branch of the reference's CPU attention: "
-                          f"5 of 25 windows x {heads} heads ({tw:.3f} s) and 2 of {heads} global heads ({tg:.3f} s), "
-                          f"scaled to {depth - ng_} windowed and {ng_} global layers")
+                          f"one whole windowed layer, {WINDOWS} windows x {heads} heads ({tw:.3f} s), and one whole "
+                          f"global layer, {heads} heads ({tg:.3f} s), best of 2, times {depth - ng_} windowed and "
+                          f"{ng_} global layers")
             for batch in (1, 4, 8):
                 res[f"sweep_{mname}_attention_b{batch}_f16"]["cpu_baseline"] = leg
 
