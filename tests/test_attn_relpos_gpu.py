@@ -322,6 +322,37 @@ def test_argument_errors_are_reported(hip):
                              torch.zeros(8, 8, device="cuda", dtype=torch.float64), 2, 3, 0.3)
 
 
+def test_the_switch_on_device_tensors(hip):
+    """set_enabled(False) (cpu_gemm::set_enabled's counterpart): a call raises SamHipDisabled and
+    launches nothing, so the output buffer keeps what it held; set_enabled(True) gives the ordinary
+    result again, equal to a call made before the switch."""
+    g = torch.Generator(device="cuda").manual_seed(8)
+    h = w = 14
+    q = torch.randn(4, h * w, 80, device="cuda", generator=g).half()
+    kt = torch.randn(4, 80, h * w, device="cuda", generator=g).half()
+    v = torch.randn(4, h * w, 80, device="cuda", generator=g).half()
+    table = (0.02 * torch.randn(4 * h - 2, 80, device="cuda", generator=g)).half()
+    want = hip.attention_relpos(q, kt, v, table, h, w, 80 ** -0.5)
+    L = hip.load()
+    out = torch.full_like(q, 7.0)
+    try:
+        hip.set_enabled(False)
+        assert not hip.enabled()
+        with pytest.raises(hip.SamHipDisabled, match="switched off"):
+            hip.attention_relpos(q, kt, v, table, h, w, 80 ** -0.5)
+        rc = L.sam_hip_attn_relpos(q.data_ptr(), kt.data_ptr(), v.data_ptr(), table.data_ptr(), out.data_ptr(), 1, 4,
+                                   h, w, 80, 80 ** -0.5, None)
+        assert rc == 5
+        torch.cuda.synchronize()
+        assert bool((out == 7.0).all())
+    finally:
+        hip.set_enabled(True)
+    assert hip.enabled()
+    got = hip.attention_relpos(q, kt, v, table, h, w, 80 ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_misaligned_operands_are_rejected(hip):
     """The kernels move q, kT, v, the table and out in 16-byte vectors, so the C ABI rejects pointers
     that are not 16-byte aligned instead of running on them. A view that starts one element into a
