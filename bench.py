@@ -609,6 +609,35 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
             res[f"vit_h_qkv_split_{name}_f16"]["cpu_baseline"] = cpu_leg(
                 tcpu, 1, 1e6, "us", "the whole block on cpu::QkvSplit (kernels.rs:239-263, f32), best of 3")
 
+    # qkv_rope of a SAM 3 ViT block (f16): the fused qkv projection's output [5184, 3 x 1024] plus bias,
+    # 2-D RoPE on q and k, packed [3, T, 16, 64]; windowed blocks use 24x24-token tables (9 windows of a
+    # 72x72 grid), global blocks one 72x72 table.
+    for name, n in (("window", 576), ("global", 5184)):
+        tok, c3 = 5184, 3 * 1024
+        y = torch.randn(tok, c3, device=dev, generator=g).half()
+        bq = torch.randn(c3, device=dev, generator=g).half()
+        cs = torch.rand(n, 64, device=dev, generator=g)
+        sn = torch.rand(n, 64, device=dev, generator=g)
+        packed = torch.empty(3, tok, 16, 64, device=dev, dtype=torch.float16)
+        nbytes = 2.0 * tok * c3 * 2 + 2 * n * 64 * 4
+        run = Cycle(cold_sets(nbytes, y, packed),
+                    lambda y_, pk: check(lib, lib.sam_hip_qkv_rope(y_.data_ptr(), bq.data_ptr(), cs.data_ptr(),
+                                                                   sn.data_ptr(), pk.data_ptr(), 1, tok, n, 16, 64,
+                                                                   sp)))
+        ms = timer.avg_ms(run, 50)
+        del run
+        res[f"sam3_qkv_rope_{name}_f16"] = {
+            "workload": f"SAM 3 ViT qkv_rope, {tok} tokens (tables of {n} rows) x 16 heads x 64, f16",
+            "us": round(ms * 1e3, 2), "compulsory_bytes": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        if cpu:
+            yh, bh_, ch, sh = host(y), host(bq), host(cs), host(sn)
+            tcpu = best_of(lambda: orc.qkv_rope(yh, bh_, ch, sh, n, 16, 64, nthreads=cores), 3)
+            res[f"sam3_qkv_rope_{name}_f16"]["cpu_baseline"] = cpu_leg(
+                tcpu, 1, 1e6, "us", "the whole block on cpu::QkvRope (kernels.rs:321-362, f32), best of 3")
+
     # The elementwise steps beside attention in a ViT-H block, f16: the projection output plus bias plus
     # the residual (4096 tokens x 1280), and the MLP's bias + exact GELU (4096 x 5120).
     for name, (rows, cols) in (("bias_residual", (4096, 1280)), ("bias_gelu", (4096, 5120))):

@@ -259,6 +259,21 @@ int sam_hip_rope(const void* x, const float* rope_cos, const float* rope_sin, vo
                  int h, int d, const long* strides_x, const long* strides_out, int rope_rows, int n_rot,
                  void* stream);
 
+/*
+ * SAM 3 ViT's qkv step: the fused qkv projection's output with the bias added and 2-D RoPE on q and k,
+ * packed for the attention:
+ *   y [tokens, 3*nh*hd] (columns (qkv, head, d)), bias [3*nh*hd], rope_cos/rope_sin f32 [n, hd]
+ *   -> out [3, tokens, nh, hd]; for a q or k pair (x0, x1) = (y + bias)[2i, 2i+1] of token t,
+ *   out = (x0*c - x1*s, x1*c + x0*s) with c, s = cos/sin[t % n, 2i] (the even column serves both);
+ *   v rows are y + bias.
+ * In f32, y + bias unrounded, each product and the difference (sum) rounded, converted to dtype once.
+ * Replaces kernels::qkv_rope (kernels.rs:1013-1037; GPU op kernels.rs:1330-1362, sam.cu:210-235; CPU
+ * twin kernels.rs:321-362); the tables are those of rope_tables_hd (sam3/vision.rs:26-46).
+ * Limits: hd even; 3*nh*hd < 2^31; pointers 16-byte aligned. hd % 8 == 0 runs the vector kernel.
+ */
+int sam_hip_qkv_rope(const void* y, const void* bias, const float* rope_cos, const float* rope_sin, void* out,
+                     int dtype, long tokens, int n, int nh, int hd, void* stream);
+
 /* Message describing the last error returned on this thread ("" if none). */
 const char* sam_hip_last_error(void);
 

@@ -146,6 +146,38 @@ void oracle_qkv_split(const float* y, const float* bias, float* out, long tokens
   }
 }
 
+/* kernels.rs:321-362 (cpu::QkvRope; the GPU op sam.cu:210-235 has the same data flow). Per token t, with
+ * (x0, x1) = y + bias of a pair in f32: q and k pairs become (x0*cs - x1*sn, x1*cs + x0*sn) with
+ * cs, sn the table's even column 2j of row t % n (kernels.rs:348), each product and the difference
+ * rounded (this file is built without FMA contraction); v pairs stay x0, x1. out is [3, tokens, c]. */
+void oracle_qkv_rope(const float* y, const float* bias, const float* cos_t, const float* sin_t, float* out,
+                     long tokens, int n, int nh, int hd, int nthreads) {
+  const long c = (long)nh * hd;
+#pragma omp parallel for schedule(static) num_threads(threads_or_all(nthreads))
+  for (long t = 0; t < tokens; ++t) {
+    const long tok = t % n;
+    for (int which = 0; which < 3; ++which) {
+      const float* src = y + t * 3 * c + which * c;
+      const float* b = bias + which * c;
+      float* dst = out + which * tokens * c + t * c;
+      for (int h = 0; h < nh; ++h) {
+        for (int j = 0; j < hd / 2; ++j) {
+          const long i = (long)h * hd + 2 * j;
+          const float x0 = src[i] + b[i], x1 = src[i + 1] + b[i + 1];
+          if (which < 2) {
+            const float cs = cos_t[tok * hd + 2 * j], sn = sin_t[tok * hd + 2 * j];
+            dst[i] = x0 * cs - x1 * sn;
+            dst[i + 1] = x1 * cs + x0 * sn;
+          } else {
+            dst[i] = x0;
+            dst[i + 1] = x1;
+          }
+        }
+      }
+    }
+  }
+}
+
 void oracle_deform_attn(const float* value, const float* loc, const float* attn, float* out, int b, int s, int q, int h,
                         int d, int l, int p, const int* shapes, int nthreads) {
   long starts[64];

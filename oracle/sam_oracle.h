@@ -38,6 +38,11 @@ void oracle_attention_relpos(const float* q, const float* kt, const float* v, co
  * q [bh,n,hd], kT [bh,hd,n], v [bh,n,hd] back to back, bh = tokens/n*nh. */
 void oracle_qkv_split(const float* y, const float* bias, float* out, long tokens, int n, int nh, int hd, int nthreads);
 
+/* kernels.rs:321-362 (cpu::QkvRope). y [tokens, 3*nh*hd], bias [3*nh*hd], cos/sin [n, hd] -> out
+ * [3, tokens, nh*hd]: bias added, q and k pairs rotated by row t % n of the tables (even columns). */
+void oracle_qkv_rope(const float* y, const float* bias, const float* cos_t, const float* sin_t, float* out,
+                     long tokens, int n, int nh, int hd, int nthreads);
+
 /* kernels.rs:776-818 (cpu::DeformAttn). value [b,s,h,d], loc [b,q,h,l,p,2], attn [b,q,h,l,p],
  * shapes = l (height,width) pairs -> out [b,q,h*d]. */
 void oracle_deform_attn(const float* value, const float* loc, const float* attn, float* out, int b, int s, int q, int h,

@@ -41,6 +41,7 @@ def lib():
                                               ctypes.c_int, ctypes.c_float, ctypes.c_int]
         L.oracle_qkv_split.argtypes = [_F, _F, _F, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_int]
+        L.oracle_qkv_rope.argtypes = [_F] * 5 + [ctypes.c_long] + [ctypes.c_int] * 4
         L.oracle_deform_attn.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 7 + [_I, ctypes.c_int]
         L.oracle_deform_prep.argtypes = [_F] * 5 + [ctypes.c_int] * 6 + [_I, ctypes.c_int, ctypes.c_int]
         L.oracle_sdpa.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 6
@@ -105,6 +106,19 @@ def qkv_split(y, bias, n: int, nh: int, hd: int, nthreads: int = 0):
     lib().oracle_qkv_split(_p(y), _p(bias), _p(out), t, n, nh, hd, nthreads)
     bh = t // n * nh
     return out[0].reshape(bh, n, hd), out[1].reshape(bh, hd, n), out[2].reshape(bh, n, hd)
+
+
+def qkv_rope(y, bias, cos, sin, n: int, nh: int, hd: int, dtype: str = "f32", nthreads: int = 0) -> np.ndarray:
+    """kernels.rs:321-362 (and the GPU op sam.cu:210-235). y [T, 3*nh*hd] and bias [3*nh*hd] holding
+    values of `dtype`, cos/sin f32 [n, hd] -> packed [3, T, nh, hd]: the f32 result of the reference's
+    arithmetic, converted to `dtype` once at the end as the GPU op stores it."""
+    y, bias, cos, sin = _f32(y), _f32(bias), _f32(cos), _f32(sin)
+    t = y.shape[0]
+    assert y.shape == (t, 3 * nh * hd) and bias.shape == (3 * nh * hd,) and hd % 2 == 0
+    assert cos.shape == (n, hd) and sin.shape == (n, hd)
+    out = np.empty((3, t, nh, hd), np.float32)
+    lib().oracle_qkv_rope(_p(y), _p(bias), _p(cos), _p(sin), _p(out), t, n, nh, hd, nthreads)
+    return out if dtype == "f32" else round_to(out, dtype)
 
 
 def deform_attn(value, loc, attn, shapes, nthreads: int = 0) -> np.ndarray:

@@ -32,7 +32,7 @@ SOURCES = [
     "relpos_softmax.hip",
     "qkv_split.hip",
     "flash_attn.hip", "flash_attn_d256.hip", "flash_attn_f32.hip", "flash_noalloc.hip",
-    "rope.hip",
+    "rope.hip", "qkv_rope.hip",
     "sam_hip_abi.cpp",
 ]
 

@@ -30,6 +30,8 @@ hipError_t qkv_split_grid(int dtype, const void* y, const void* bias, void* out,
                           int nh, int hd, hipStream_t stream);
 hipError_t window_merge(int dtype, const void* ctx, void* out, int batch, int gh, int gw, int ws, int nh, int hd,
                         hipStream_t stream);
+hipError_t qkv_rope(int dtype, const void* y, const void* bias, const float* cos_t, const float* sin_t, void* out,
+                    long tokens, int n, int nh, int hd, hipStream_t stream);
 hipError_t preprocess(int dtype, const void* img, void* out, int h, int w, int nh, int nw, int size, const float* mean,
                       const float* stdv, hipStream_t stream);
 int preprocess_max_taps(int n, int nout);
@@ -101,7 +103,7 @@ int report_error(int code, const std::string& msg) {
 
 extern "C" {
 
-int sam_hip_abi_version(void) { return 4; }
+int sam_hip_abi_version(void) { return 5; }
 
 void sam_hip_set_enabled(int on) { g_enabled.store(on != 0, std::memory_order_relaxed); }
 
@@ -578,6 +580,28 @@ int sam_hip_rope(const void* x, const float* cos_t, const float* sin_t, void* ou
   return check_launch(samhip::rope_rows(dtype, x, sx, out, so, b, l, h, d, cos_t, sin_t, rope_rows, n_rot,
                                         reinterpret_cast<hipStream_t>(stream)),
                       "rope");
+}
+
+int sam_hip_qkv_rope(const void* y, const void* bias, const float* cos_t, const float* sin_t, void* out, int dtype,
+                     long tokens, int n, int nh, int hd, void* stream) {
+  SAM_HIP_REQUIRE_ENABLED("qkv-rope");
+  if (!y || !bias || !cos_t || !sin_t || !out) return fail(SAM_HIP_EINVAL, "qkv-rope: null pointer argument");
+  if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
+  if (tokens <= 0 || n <= 0 || nh <= 0 || hd <= 0)
+    return fail(SAM_HIP_EINVAL, "qkv-rope: sizes must be positive (tokens=%ld n=%d nh=%d hd=%d)", tokens, n, nh, hd);
+  if (hd % 2 != 0) return fail(SAM_HIP_EINVAL, "qkv-rope: head dim must be even (RoPE rotates pairs), got %d", hd);
+  if (3L * nh * hd > 0x7fffffffL)  // the kernels' column arithmetic is 32-bit
+    return fail(SAM_HIP_EUNSUPPORTED, "qkv-rope: 3*nh*hd = %ld columns is beyond 2^31", 3L * nh * hd);
+  // the vector kernel (hd % 8 == 0) counts its threads, at most one per 8-column vector, in 32 bits; the
+  // pair kernel's grid is 32-bit
+  const long units = hd % 8 == 0 ? tokens * (3L * nh * hd / 8) : tokens * (3L * nh * hd / 2);
+  if (units >= (hd % 8 == 0 ? (1L << 32) : (1L << 39)) || (long)n * hd >= (1L << 40))
+    return fail(SAM_HIP_EUNSUPPORTED, "qkv-rope: too many tokens (%ld)", tokens);
+  if (!aligned16(y) || !aligned16(bias) || !aligned16(cos_t) || !aligned16(sin_t) || !aligned16(out))
+    return fail(SAM_HIP_EUNSUPPORTED, "qkv-rope: y, bias, cos, sin and out must be 16-byte aligned");
+  return check_launch(
+      samhip::qkv_rope(dtype, y, bias, cos_t, sin_t, out, tokens, n, nh, hd, reinterpret_cast<hipStream_t>(stream)),
+      "qkv-rope");
 }
 
 }  // extern "C"

@@ -89,6 +89,8 @@ def load():
         L.sam_hip_flash_attn_noalloc.restype = _i
         L.sam_hip_rope.argtypes = [_vp] * 4 + [_i] * 5 + [_lp] * 2 + [_i, _i, _vp]
         L.sam_hip_rope.restype = _i
+        L.sam_hip_qkv_rope.argtypes = [_vp] * 5 + [_i, ctypes.c_long, _i, _i, _i, _vp]
+        L.sam_hip_qkv_rope.restype = _i
         L.sam_hip_sdpa_mask.argtypes = [_vp] * 5 + [_i] * 6 + [_lp] * 5 + [_f, _vp, ctypes.c_long, _vp]
         L.sam_hip_sdpa_mask.restype = _i
         L.sam_hip_set_enabled.argtypes = [_i]
@@ -509,6 +511,26 @@ def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_rot: int | Non
     _check(load().sam_hip_rope(x4.data_ptr(), cos.data_ptr(), sin.data_ptr(), out.data_ptr(), dt, b, l, h, d,
                                _strides_blhd(x4, "blhd"), None, cos.shape[0], n_rot, _stream()))
     return out.squeeze(2) if squeeze else out
+
+
+def qkv_rope(y: torch.Tensor, bias: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n: int, heads: int,
+             hd: int) -> torch.Tensor:
+    """kernels::qkv_rope (kernels.rs:1013-1037): y [T, 3*heads*hd] (bias-free fused qkv projection) + bias,
+    2-D RoPE on q and k with f32 tables [n, hd] (token t uses row t % n) -> packed [3, T, heads, hd]."""
+    y = y.contiguous()
+    _contig(y, bias)
+    dt = _dtype(y, bias)
+    t = y.shape[0]
+    if y.dim() != 2 or y.shape[1] != 3 * heads * hd or bias.shape != (3 * heads * hd,):
+        raise SamHipError(f"qkv_rope: y must be [T, {3 * heads * hd}] and bias [{3 * heads * hd}], "
+                          f"got {tuple(y.shape)} and {tuple(bias.shape)}")
+    cos, sin = _rope_tables(cos, sin, hd, y.device)
+    if cos.shape[0] != n:
+        raise SamHipError(f"qkv_rope: tables must have n = {n} rows, got {cos.shape[0]}")
+    out = torch.empty((3, t, heads, hd), dtype=y.dtype, device=y.device)
+    _check(load().sam_hip_qkv_rope(y.data_ptr(), bias.data_ptr(), cos.data_ptr(), sin.data_ptr(), out.data_ptr(), dt,
+                                   t, n, heads, hd, _stream()))
+    return out
 
 
 def rope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,

@@ -120,6 +120,28 @@ def test_column_counts_beyond_int_are_refused(lib):
     assert lib.sam_hip_window_merge(fake, fake, 1, 1, 1, 1, 1, nh2, 8, None) == 3
 
 
+def test_qkv_rope_argument_checks(lib):
+    """sam_hip_qkv_rope rejects null pointers, non-positive sizes, an odd head dim (RoPE rotates pairs),
+    column counts beyond 2^31, too many vectors and misaligned pointers, before any launch."""
+    lib.sam_hip_last_error.restype = ctypes.c_char_p
+    vp, i, lg = ctypes.c_void_p, ctypes.c_int, ctypes.c_long
+    fn = lib.sam_hip_qkv_rope
+    fn.argtypes, fn.restype = [vp] * 5 + [i, lg, i, i, i, vp], i
+    fake = vp(0x1000)
+    assert fn(fake, fake, None, fake, fake, 1, 5184, 576, 16, 64, None) == 1
+    assert fn(fake, fake, fake, fake, fake, 3, 5184, 576, 16, 64, None) == 2
+    assert fn(fake, fake, fake, fake, fake, 1, 0, 576, 16, 64, None) == 1
+    assert fn(fake, fake, fake, fake, fake, 1, 5184, 0, 16, 64, None) == 1
+    assert fn(fake, fake, fake, fake, fake, 1, 5184, 576, 16, 63, None) == 1
+    assert b"even" in lib.sam_hip_last_error()
+    assert fn(fake, fake, fake, fake, fake, 1, 1, 1, 1 << 22, 256, None) == 3
+    assert b"beyond 2^31" in lib.sam_hip_last_error()
+    assert fn(fake, fake, fake, fake, fake, 1, 1 << 31, 576, 16, 64, None) == 3  # 2^31 * 384 vectors
+    assert b"too many tokens" in lib.sam_hip_last_error()
+    assert fn(fake, vp(0x1008), fake, fake, fake, 1, 5184, 576, 16, 64, None) == 3
+    assert b"aligned" in lib.sam_hip_last_error()
+
+
 def test_the_switch_turns_every_entry_point_off_and_on(lib):
     """sam_hip_set_enabled mirrors cpu_gemm::set_enabled (cpu_gemm.rs:25-32): while it is off, every
     compute entry point returns SAM_HIP_EDISABLED (5) before reading its arguments (null pointers and
@@ -145,6 +167,7 @@ def test_the_switch_turns_every_entry_point_off_and_on(lib):
         "sam_hip_flash_attn_noalloc": [vp] * 4 + [i] * 6 + [lp] * 4 + [f, vp, vp, i, i, i, vp],
         "sam_hip_sdpa_mask": [vp] * 5 + [i] * 6 + [lp] * 5 + [f, vp, ctypes.c_long, vp],
         "sam_hip_rope": [vp] * 4 + [i] * 5 + [lp] * 2 + [i, i, vp],
+        "sam_hip_qkv_rope": [vp] * 5 + [i, ctypes.c_long, i, i, i, vp],
     }
     # every declared compute entry point is covered
     queries = {"sam_hip_flash_attn_workspace_size", "sam_hip_last_error", "sam_hip_abi_version",

@@ -480,6 +480,132 @@ def test_rope_attention_matches_composed_float64(oracle_lib):
     assert np.abs(got - want).max() < 5e-5
 
 
+# ----------------------------------------------------------------------------------------- qkv_rope
+# Pins of oracle.qkv_rope (kernels.rs:321-362): the identity and quarter-turn tables fix the formula's
+# terms and signs exactly, the q/k planes agree bit for bit with the separately pinned rope (the same
+# rounding of each product and the sum), tables with NaN odd columns show only the even column is read,
+# and period-n rows show the t % n row rule. _qkv_rope_checks runs all of them on an implementation;
+# the mutant test plants one plausible mistake per copy and checks that some pin rejects it.
+
+def _qkv_rope_inputs(t, n, nh, hd, seed):
+    r = _rng(seed)
+    y = r.standard_normal((t, 3 * nh * hd)).astype(np.float32)
+    b = r.standard_normal(3 * nh * hd).astype(np.float32)
+    return y, b
+
+
+def _qkv_rope_checks(oracle_lib, impl):
+    """Returns the names of the pins that `impl(y, b, cos, sin, n, nh, hd) -> [3, T, nh, hd]` fails."""
+    failed = []
+    t, n, nh, hd = 11, 4, 3, 8
+    y, b = _qkv_rope_inputs(t, n, nh, hd, 31)
+    x = (y + b).reshape(t, 3, nh, hd).transpose(1, 0, 2, 3)
+    ones, zeros = np.ones((n, hd), np.float32), np.zeros((n, hd), np.float32)
+    if not np.array_equal(impl(y, b, ones, zeros, n, nh, hd), x):
+        failed.append("identity")
+    quarter = x.copy()
+    quarter[:2, ..., 0::2], quarter[:2, ..., 1::2] = -x[:2, ..., 1::2], x[:2, ..., 0::2]
+    if not np.array_equal(impl(y, b, zeros, ones, n, nh, hd), quarter):
+        failed.append("quarter turn")
+    side = 2  # n = 4 tokens per window, the rope_tables_hd tables
+    cos, sin = oracle_lib.rope_tables(side, 1.0, hd, 100.0)
+    got = impl(y, b, cos, sin, n, nh, hd)
+    rows = np.arange(t) % n
+    for which in range(2):
+        for h in range(nh):
+            want = oracle_lib.rope(x[which, :, h], cos[rows], sin[rows])
+            if not np.array_equal(got[which, :, h], want):
+                failed.append("rope")
+    if not np.array_equal(got[2], x[2]):
+        failed.append("v plane")
+    r = _rng(32)
+    cr, sr = r.standard_normal((n, hd)).astype(np.float32), r.standard_normal((n, hd)).astype(np.float32)
+    cr[:, 1::2] = np.nan
+    sr[:, 1::2] = np.nan
+    yp = np.tile(y[:n], (3, 1))[:t]  # rows t and t + n equal
+    gp = impl(yp, b, cr, sr, n, nh, hd)
+    if not np.all(np.isfinite(gp)):
+        failed.append("even column")
+    if not np.array_equal(gp[:, n:], gp[:, :t - n]):
+        failed.append("period n")
+    return failed
+
+
+def test_qkv_rope_passes_every_pin(oracle_lib):
+    assert _qkv_rope_checks(oracle_lib, oracle_lib.qkv_rope) == []
+
+
+def test_qkv_rope_matches_float64_rotation(oracle_lib):
+    t, n, nh, hd = 40, 16, 2, 32
+    cos, sin = oracle_lib.rope_tables(4, 1.0, hd, 10000.0)
+    y, b = _qkv_rope_inputs(t, n, nh, hd, 33)
+    got = oracle_lib.qkv_rope(y, b, cos, sin, n, nh, hd)
+    x = (y.astype(np.float64) + b).reshape(t, 3, nh, hd)
+    cis = refimpl.axial_rope_cis64(4, hd, 10000.0)[np.arange(t) % n]
+    for which in range(2):
+        for h in range(nh):
+            want = refimpl.rope_complex64(x[:, which, h], cis)
+            assert np.abs(got[which, :, h] - want).max() < 4e-6 * (1 + np.abs(want).max())
+    np.testing.assert_allclose(got[2], x[:, 2], rtol=1e-7, atol=1e-6)
+
+
+def test_qkv_rope_output_rounding_is_round_to_nearest_even(oracle_lib):
+    t, n, nh, hd = 6, 3, 2, 8
+    cos, sin = oracle_lib.rope_tables(2, 1.0, hd, 100.0)
+    y, b = _qkv_rope_inputs(t, n, nh, hd, 34)
+    y, b = oracle_lib.round_to(y, "bf16"), oracle_lib.round_to(b, "bf16")
+    f32 = oracle_lib.qkv_rope(y, b, cos[:n], sin[:n], n, nh, hd)
+    assert np.array_equal(oracle_lib.qkv_rope(y, b, cos[:n], sin[:n], n, nh, hd, dtype="bf16"),
+                          oracle_lib.round_to(f32, "bf16"))
+
+
+def _qkv_rope_mutants():
+    def base(y, b, cos, sin, n, nh, hd, odd=False, row=lambda t, n: t % n, sign=1.0, rot_v=False, fma=False,
+             pre_round=False):
+        t = y.shape[0]
+        x = (y + b).reshape(t, 3, nh * hd).transpose(1, 0, 2).copy()
+        if pre_round:  # the bias sum rounded to bf16 first (the CPU tensor fallback's order)
+            x = (x.view(np.uint32) + 0x7FFF + ((x.view(np.uint32) >> 16) & 1) & 0xFFFF0000).view(np.float32)
+        out = x.copy()
+        for tt in range(t):
+            rr = row(tt, n)
+            c = np.tile(cos[rr, 1::2] if odd else cos[rr, 0::2], nh)
+            s = sign * np.tile(sin[rr, 0::2], nh)
+            for which in range(3 if rot_v else 2):
+                x0, x1 = x[which, tt, 0::2], x[which, tt, 1::2]
+                if fma:
+                    out[which, tt, 0::2] = (x0.astype(np.float64) * c - (x1 * s)).astype(np.float32)
+                else:
+                    out[which, tt, 0::2] = x0 * c - x1 * s
+                out[which, tt, 1::2] = x1 * c + x0 * s
+        return out.reshape(3, t, nh, hd)
+
+    def odd_column(*a):
+        return base(*a, odd=True)
+
+    def row_not_modulo(*a):
+        return base(*a, row=lambda t, n: min(t, n - 1))
+
+    def sin_sign_flipped(*a):
+        return base(*a, sign=-1.0)
+
+    def v_rotated(*a):
+        return base(*a, rot_v=True)
+
+    def fused_first_product(*a):
+        return base(*a, fma=True)
+
+    def bias_sum_rounded(*a):
+        return base(*a, pre_round=True)
+
+    return [odd_column, row_not_modulo, sin_sign_flipped, v_rotated, fused_first_product, bias_sum_rounded]
+
+
+@pytest.mark.parametrize("mutant", _qkv_rope_mutants(), ids=lambda f: f.__name__)
+def test_qkv_rope_mutants_are_caught(oracle_lib, mutant):
+    assert _qkv_rope_checks(oracle_lib, mutant) != []
+
+
 # ----------------------------------------------------------------------------------------- helpers
 
 def test_rounding_helpers_are_round_to_nearest_even(oracle_lib):
