@@ -446,7 +446,8 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
   // ---- 4. normalise and store: lane holds O^T[32*ob + 8*a + 4*hh + b][query n]. The wave's 32 output
   // rows are consecutive in memory, so they go through LDS (its own q rows in buffer 1, free since the
   // barrier before tile 3) as the [32][hd] image of that range and leave as contiguous 1 KB stores of
-  // 16-byte pieces. At hd 64 (128-byte rows) the 16-byte chunk c of row r sits at chunk c ^ (r & 7), so
+  // 16-byte pieces, non-temporal: whole lines that nothing in the launch reads again (ViT-H window
+  // layer 19.9 -> 19.0 us; the global kernel's 8-byte row pieces lose with the same hint). At hd 64 (128-byte rows) the 16-byte chunk c of row r sits at chunk c ^ (r & 7), so
   // the 32 rows a store instruction covers spread over the banks.
   if (active) {
     const float inv = 1.f / sum_with_partner32(l_run);
@@ -471,7 +472,7 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
     for (int i = 0; i < 32 * HD * (int)sizeof(T) / 1024; ++i) {
       const int b = 1024 * i + 16 * lane;
       const int sb = HD == 64 ? (b & ~127) + 16 * (((b >> 4) & 7) ^ ((b >> 7) & 7)) : b;
-      if (b < nbytes) *reinterpret_cast<u32x4*>(dst + b) = *reinterpret_cast<const u32x4*>(src + sb);
+      if (b < nbytes) __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(src + sb), reinterpret_cast<u32x4*>(dst + b));
     }
   }
 }
