@@ -52,13 +52,16 @@ int sam_hip_enabled(void);
  * Replaces, in one kernel, the reference's GPU sequence bmm(q, kT) -> relpos_softmax -> bmm(P, v)
  * (sam1/encoder.rs:79-82; kernels.rs:12-43, 919-924, 1108-1149) and is the GPU counterpart of
  * attention_relpos_cpu (kernels.rs:899-906).
- * Limits: 1 <= h, w <= 64; hd % 8 == 0 and hd <= 128 (f16/bf16), hd % 4 == 0 and hd <= 128 (f32).
- * Which kernel runs (f16/bf16) is chosen for speed only; every shape within the limits gets the same
- * result to the same tolerance. Dedicated kernels take SAM's two shapes at hd 64 and 80: windows with
- * 13 <= h <= 16 and an even w <= 16, and the 64-column global grid (w == 64, h <= 64) when
- * 2^-6 <= scale * log2(e) <= 4 (SAM's hd^-0.5 * log2(e) is 0.16-0.18). Every other shape or scale runs
- * on the general kernel, at a lower speed. In f32, hd 64 has its own window kernel (w <= 16, h <= 16,
- * h*w <= 256) and global kernel (w == 64); other f32 shapes run on the general f32 kernel.
+ * Limits: f16/bf16 1 <= h, w <= 128, hd % 8 == 0 and hd <= 128; f32 1 <= h, w <= 64, hd % 4 == 0 and
+ * hd <= 128. Which kernel runs (f16/bf16) is chosen for speed only; every shape within the limits gets
+ * the same result to the same tolerance. Dedicated kernels take SAM's two shapes at hd 64 and 80:
+ * windows with 13 <= h <= 16 and an even w <= 16, and the 64-column global grid (w == 64, h <= 64) when
+ * 2^-6 <= scale * log2(e) <= 4 (SAM's hd^-0.5 * log2(e) is 0.16-0.18). Every other shape or scale up to
+ * 64 x 64 runs on the general kernel, and grids past 64 rows or columns on a kernel that walks them in
+ * 64-column passes, each at a lower speed. The reference's own GPU sequence stops at h*w <= 8192 (the
+ * relpos_softmax row limit); here the scores stay on chip, so every h, w <= 128 runs. In f32, hd 64 has
+ * its own window kernel (w <= 16, h <= 16, h*w <= 256) and global kernel (w == 64); other f32 shapes run
+ * on the general f32 kernel.
  */
 int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void* table, void* out, int dtype,
                         int bh, int h, int w, int hd, float scale, void* stream);

@@ -24,7 +24,7 @@ PROBE_SOURCES = ["gather_probe.hip"]
 
 SOURCES = [
     "attn_relpos.hip",
-    "attn_relpos_win.hip", "attn_relpos_glob.hip",
+    "attn_relpos_win.hip", "attn_relpos_glob.hip", "attn_relpos_wide.hip",
     "attn_relpos_f32.hip",
     "deform_attn.hip",
     "preprocess.hip",

@@ -389,9 +389,17 @@ __global__ __launch_bounds__(NWV * 64) void attn_relpos_kernel(const T* __restri
         for (int j = 0; j < 8; ++j) {
           const float x = s_cur[u >> 1][8 * (u & 1) + j];
           pv[j] = exp2_fast(POS ? fmaf(x, sc, c[u >> 1]) : x + c[u >> 1]);
-          if (!kOnes) lsum += pv[j];
+          if (!kOnes && kSplitP) lsum += pv[j];  // bf16: P.V takes hi + lo, P itself to ~16 bits
         }
         b[u] = pack8(pv, (X8*)nullptr);
+        if constexpr (!kOnes && !kSplitP) {
+          // f16: the sum over P as the P.V product sees it (rounded), as the ones row gives it when hd
+          // leaves a spare O^T row: numerator and denominator weigh each key alike
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+          for (int j = 0; j < 8; j += 2)
+            lsum = __builtin_amdgcn_fdot2(h2{b[u][j], b[u][j + 1]}, h2{(f16)1.f, (f16)1.f}, lsum, false);
+        }
         if (kSplitP) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) pv[j] -= to_f32(b[u][j]);
@@ -526,15 +534,20 @@ static hipError_t pick_hd(const void* q, const void* kt, const void* v, const vo
   return pick_mode<T, 128>(q, kt, v, table, out, bh, hd, h, w, scale, stream);
 }
 
-// Shape limits are checked by the caller (sam_hip_abi.cpp): 1 <= h, w <= 64, hd % 8 == 0, hd <= 128.
+// Shape limits are checked by the caller (sam_hip_abi.cpp): 1 <= h, w <= 128, hd % 8 == 0, hd <= 128.
 bool attn_relpos_window(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                         int hd, int h, int w, float scale, hipStream_t stream, hipError_t* err);
 bool attn_relpos_global(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                         int hd, int h, int w, float scale, hipStream_t stream, hipError_t* err);
 
+hipError_t attn_relpos_wide(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out,
+                            int bh, int hd, int h, int w, float scale, hipStream_t stream);
+
 hipError_t attn_relpos_half(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out,
                             int bh, int hd, int h, int w, float scale, hipStream_t stream) {
   hipError_t e;
+  // grids past 64 rows or columns (up to 128): attn_relpos_wide.hip
+  if (h > 64 || w > 64) return attn_relpos_wide(dtype, q, kt, v, table, out, bh, hd, h, w, scale, stream);
   // windowed grids (the 14x14 SAM windows): attn_relpos_win.hip; the 64-column global grid:
   // attn_relpos_glob.hip; every other shape: the general kernel below
   if (attn_relpos_window(dtype, q, kt, v, table, out, bh, hd, h, w, scale, stream, &e)) return e;

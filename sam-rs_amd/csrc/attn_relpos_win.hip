@@ -397,9 +397,17 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         pv[e] = exp2_fast(fmaf(s[w4 >> 1][8 * (w4 & 1) + e], sc, c[w4 >> 1]));
-        lsum += pv[e];
+        if (kSplitP) lsum += pv[e];  // bf16: P.V takes hi + lo, P itself to ~16 bits
       }
       b[w4] = pack8(pv, (X8*)nullptr);
+      if constexpr (!kSplitP) {
+        // f16: the denominator sums P as the P.V product sees it (rounded), so that numerator and
+        // denominator weigh each key alike: v_dot2 of the packed P with ones, accumulated in f32
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+          lsum = __builtin_amdgcn_fdot2(h2{b[w4][e], b[w4][e + 1]}, h2{(f16)1.f, (f16)1.f}, lsum, false);
+      }
       if (kSplitP) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) pv[e] -= to_f32(b[w4][e]);

@@ -118,8 +118,9 @@ int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void
   if (!dtype_ok(dtype)) return fail(SAM_HIP_EDTYPE, "unsupported dtype %d for a sam-rs HIP kernel", dtype);
   if (bh <= 0 || h <= 0 || w <= 0 || hd <= 0)
     return fail(SAM_HIP_EINVAL, "attn-relpos: sizes must be positive (bh=%d h=%d w=%d hd=%d)", bh, h, w, hd);
-  if (h > 64 || w > 64)
-    return fail(SAM_HIP_EUNSUPPORTED, "attn-relpos: the fused kernel supports grids up to 64x64, got %dx%d", h, w);
+  if (h > 128 || w > 128 || (dtype == 0 && (h > 64 || w > 64)))
+    return fail(SAM_HIP_EUNSUPPORTED, "attn-relpos: the fused kernels support grids up to %s, got %dx%d",
+                dtype == 0 ? "64x64 in f32" : "128x128", h, w);
   const int align = dtype == 0 ? 4 : 8;
   if (hd % align != 0 || hd > 128)
     return fail(SAM_HIP_EUNSUPPORTED, "attn-relpos: head dim must be a multiple of %d and at most 128, got %d", align,

@@ -305,13 +305,13 @@ def test_heads_are_independent(hip):
 
 
 def test_argument_errors_are_reported(hip):
-    x = torch.zeros(2, 65 * 2, 16, device="cuda", dtype=torch.float16)
-    kt = torch.zeros(2, 16, 65 * 2, device="cuda", dtype=torch.float16)
-    t = torch.zeros(2 * 65 - 1 + 3, 16, device="cuda", dtype=torch.float16)
-    with pytest.raises(hip.SamHipError, match="64x64"):
-        hip.attention_relpos(x, kt, x, t, 65, 2, 0.25)
+    x = torch.zeros(2, 129 * 2, 16, device="cuda", dtype=torch.float16)
+    kt = torch.zeros(2, 16, 129 * 2, device="cuda", dtype=torch.float16)
+    t = torch.zeros(2 * 129 - 1 + 3, 16, device="cuda", dtype=torch.float16)
+    with pytest.raises(hip.SamHipError, match="128x128"):
+        hip.attention_relpos(x, kt, x, t, 129, 2, 0.25)
     with pytest.raises(hip.SamHipError, match="contiguous"):
-        hip.attention_relpos(x.transpose(1, 2), kt, x, t, 65, 2, 0.25)
+        hip.attention_relpos(x.transpose(1, 2), kt, x, t, 129, 2, 0.25)
     y = torch.zeros(1, 6, 12, device="cuda", dtype=torch.float16)
     with pytest.raises(hip.SamHipError, match="multiple of 8"):
         hip.attention_relpos(y, torch.zeros(1, 12, 6, device="cuda", dtype=torch.float16), y,
