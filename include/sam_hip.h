@@ -71,8 +71,10 @@ int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void
  *   out[b, r, k] = softmax_k(scale * s[b, r, k] + q[b,r].Th[i-kh+h-1] + q[b,r].Tw[j-kw+w-1])
  *   s [bh, h*w, h*w], q [bh, h*w, hd], table as above -> out [bh, h*w, h*w]; rows = bh*h*w.
  * The literal drop-in for kernels::relpos_softmax (kernels.rs:12-43; GPU op kernels.rs:1108-1149,
- * sam.cu:44-96) for callers that hold the score matrix. Limits: h*w <= 8192 (the reference's GPU
- * limit, kernels.rs:1078-1083), h, w <= 128, hd <= 256.
+ * sam.cu:44-96) for callers that hold the score matrix. Limits: h, w <= 128 (rows of up to 16384
+ * keys), hd <= 256. The reference's GPU kernel stops at h*w <= 8192 (kernels.rs:1078-1083) and takes
+ * its tensor path past it (kernels.rs:20-42); a binding that keeps that split bit for bit keeps its
+ * guard, one that wants the GPU past 8192 keys drops it (same formula, f32 arithmetic as below 8192).
  */
 int sam_hip_relpos_softmax(const void* s, const void* q, const void* table, void* out, int dtype, long rows, int h,
                            int w, int hd, float scale, void* stream);

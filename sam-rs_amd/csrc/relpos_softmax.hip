@@ -597,7 +597,7 @@ static hipError_t launch_relpos_softmax(const void* s, const void* q, const void
   return hipGetLastError();
 }
 
-// Checked by the caller: rows % (h*w) == 0, h*w <= 8192, h, w <= 128, hd <= 256, 16-byte aligned pointers.
+// Checked by the caller: rows % (h*w) == 0, h, w <= 128, hd <= 256, 16-byte aligned pointers.
 hipError_t relpos_softmax(int dtype, const void* s, const void* q, const void* tab, void* out, long rows, int h, int w,
                           int hd, float scale, hipStream_t stream) {
   if (dtype == kF32) return launch_relpos_softmax<float>(s, q, tab, out, rows, h, w, hd, scale, stream);

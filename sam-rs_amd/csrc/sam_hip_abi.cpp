@@ -259,9 +259,8 @@ int sam_hip_relpos_softmax(const void* s, const void* q, const void* table, void
     return fail(SAM_HIP_EINVAL, "relpos-softmax: sizes must be positive (rows=%ld h=%d w=%d hd=%d)", rows, h, w, hd);
   if (rows % ((long)h * w) != 0)
     return fail(SAM_HIP_EINVAL, "relpos-softmax: %ld rows is not a multiple of h*w = %d", rows, h * w);
-  // the reference's GPU kernel keeps a row in registers up to 256 x 32 values (kernels.rs:1078-1083)
-  if ((long)h * w > 8192)
-    return fail(SAM_HIP_EUNSUPPORTED, "relpos-softmax: rows longer than 8192 (h*w = %d)", h * w);
+  // Rows of up to 16384 keys: past 8192 (the reference's GPU kernel limit, kernels.rs:1078-1083, beyond
+  // which it takes its tensor path) they run on the two-pass scalar kernel.
   if (h > 128 || w > 128 || hd > 256)
     return fail(SAM_HIP_EUNSUPPORTED, "relpos-softmax: h, w <= 128 and hd <= 256, got %d, %d, %d", h, w, hd);
   if (rows > 0x7fffffffL) return fail(SAM_HIP_EUNSUPPORTED, "relpos-softmax: more than 2^31 rows");

@@ -107,12 +107,62 @@ def test_relpos_softmax_long_rows_f32(hip, h, w, bh, hd):
     assert e64 <= 1e-5
 
 
-def test_relpos_softmax_rejects_long_rows(hip):
-    s = torch.zeros(1, 91 * 91, 1, device="cuda", dtype=torch.float16)  # h*w = 8281 > 8192
-    q = torch.zeros(1, 91 * 91, 8, device="cuda", dtype=torch.float16)
-    t = torch.zeros(2 * 91 - 1 + 2 * 91 - 1, 8, device="cuda", dtype=torch.float16)
-    with pytest.raises(hip.SamHipError):
-        hip.relpos_softmax(s.expand(1, 91 * 91, 91 * 91), q, t, 91, 91, 0.1)
+def test_relpos_softmax_rejects_grids_past_128(hip):
+    h, w = 129, 2
+    n = h * w
+    s = torch.zeros(1, n, n, device="cuda", dtype=torch.float16)
+    q = torch.zeros(1, n, 8, device="cuda", dtype=torch.float16)
+    t = torch.zeros(2 * h - 1 + 2 * w - 1, 8, device="cuda", dtype=torch.float16)
+    with pytest.raises(hip.SamHipError, match="h, w <= 128"):
+        hip.relpos_softmax(s, q, t, h, w, 0.1)
+
+
+# Rows past the reference GPU kernel's 8192 keys (kernels.rs:1078-1083), where the reference takes its
+# tensor path and this library its two-pass scalar kernel: 96 x 96 (9216 keys) in every dtype, and the
+# 128 x 128 maximum (16384 keys) in f16. N(0,1) scores, q and table as above.
+@pytest.mark.parametrize("dtype,h,w", [("f16", 96, 96), ("bf16", 96, 96), ("f16", 128, 128), ("bf16", 90, 128)])
+def test_relpos_softmax_past_8192_keys(hip, dtype, h, w):
+    print(f"relpos_softmax long {dtype} {h}x{w}", flush=True)
+    n, hd = h * w, 8
+    r = np.random.default_rng(h * 1000 + w)
+    s = oracle.round_to(r.standard_normal((1, n, n), dtype=np.float32), dtype)
+    q = oracle.round_to(r.standard_normal((1, n, hd), dtype=np.float32), dtype)
+    t = oracle.round_to(r.standard_normal((2 * h - 1 + 2 * w - 1, hd), dtype=np.float32), dtype)
+    want = oracle.relpos_softmax(s, q, t, h, w, 0.125)
+    got = hip.relpos_softmax(dev(s, dtype), dev(q, dtype), dev(t, dtype), h, w, 0.125).float().cpu().numpy()
+    err = float(np.abs(got - want).max())
+    print(f"parity relpos_softmax {h}x{w} {dtype}: max-abs {err:.3g}", flush=True)
+    if dtype == "bf16":
+        assert (np.abs(got - want) - half_ulp_bf16(want)).max() <= 1e-3
+    else:
+        assert err <= 1e-3
+    np.testing.assert_allclose(got.sum(-1), 1.0, atol=2e-2 if dtype == "bf16" else 4e-3)
+
+
+def test_relpos_softmax_past_8192_keys_f32(hip):
+    """f32 rows of 9216 keys against a float64 evaluation on sampled rows, as for the 8192-key rows."""
+    h = w = 96
+    n, hd = h * w, 8
+    r = np.random.default_rng(4242)
+    s = r.standard_normal((1, n, n), dtype=np.float32)
+    q = r.standard_normal((1, n, hd), dtype=np.float32)
+    t = r.standard_normal((2 * h - 1 + 2 * w - 1, hd), dtype=np.float32)
+    got = hip.relpos_softmax(dev(s, "f32"), dev(q, "f32"), dev(t, "f32"), h, w, 0.125).cpu().numpy()[0]
+    rows = np.arange(0, n, 97)
+    th, tw = t[:2 * h - 1].astype(np.float64), t[2 * h - 1:].astype(np.float64)
+    exact = []
+    for rr in rows:
+        i, j = rr // w, rr % w
+        qq = q[0, rr].astype(np.float64)
+        rh = np.array([qq @ th[i - kh + h - 1] for kh in range(h)])
+        rw = np.array([qq @ tw[j - kw + w - 1] for kw in range(w)])
+        x = s[0, rr].astype(np.float64) * 0.125 + (rh[:, None] + rw[None, :]).reshape(-1)
+        e = np.exp(x - x.max())
+        exact.append(e / e.sum())
+    exact = np.array(exact)
+    e64 = np.abs(got[rows] - exact).max() / np.abs(exact).max()
+    print(f"parity relpos_softmax 96x96 f32: vs float64 {e64:.3g}", flush=True)
+    assert e64 <= 1e-5
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
