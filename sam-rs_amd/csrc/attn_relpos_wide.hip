@@ -19,16 +19,14 @@
 //     straight from global memory (16-byte A-operand pieces), so the table needs no LDS: Rw for the 64
 //     columns of the current pass, and Rh for 32 grid rows at a time (recomputed every 32 tiles), go
 //     through a wave-private scratch of 98 rows of 32 floats;
-//   * 4 waves (128 queries) per workgroup, so that the scratch and the double-buffered K/V tiles fit in
-//     LDS at every head dim up to 128.
+//   * 8 waves (256 queries, two per SIMD) per workgroup up to hd 80, 4 at hd 128, so that the scratch
+//     and the double-buffered K/V tiles fit in LDS.
 // Limits (checked by the dispatcher): 1 <= H, W <= 128, hd % 8 == 0, hd <= 128.
 #include "relpos_geom.hpp"
 
 namespace samhip {
 
 namespace wide {
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
 constexpr int kRwRows = 65;  // Rw scratch: the pass's 64 columns, then a junk row
 constexpr int kRhRows = 33;  // Rh scratch: 32 grid rows, then a junk row
 constexpr int kKStride = 64 + 16;  // K tile row stride (elements), as attn_relpos.hip
@@ -38,10 +36,10 @@ template <int HDP> struct VG {
   static constexpr int STRIDE = MBO * 32 + 16;
   static constexpr bool ONES = MBO * 32 > HDP;
 };
-template <typename T, int HDP>
+template <typename T, int HDP, int NW>
 constexpr size_t lds_bytes() {
   return (size_t)(2 * HDP * kKStride + 2 * 64 * VG<HDP>::STRIDE) * sizeof(T) +
-         (size_t)kWaves * (kRwRows + kRhRows) * 32 * sizeof(float);
+         (size_t)NW * (kRwRows + kRhRows) * 32 * sizeof(float);
 }
 template <int VK> struct KC;
 template <> struct KC<8> { typedef u32x4 type; };
@@ -54,14 +52,15 @@ __device__ __forceinline__ int wide_xcd_block(int i, int total) {
   return x * per + (x < rem ? x : rem) + j;
 }
 
-template <typename T, int HDP, int VK, bool POS>
-__global__ __launch_bounds__(wide::kThreads) void attn_relpos_wide_kernel(const T* __restrict__ q,
+template <typename T, int HDP, int VK, bool POS, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_relpos_wide_kernel(const T* __restrict__ q,
                                                                          const T* __restrict__ kt,
                                                                          const T* __restrict__ v,
                                                                          const T* __restrict__ table,
                                                                          T* __restrict__ out, int hd, int H, int W,
                                                                          float scale, int qblocks) {
   using namespace wide;
+  constexpr int kWaves = NW, kThreads = NW * 64;
   typedef KeyGeom<kRow64> G;
   typedef typename Vec<T>::x8 X8;
   constexpr bool kSplitP = __is_same(T, bf16);
@@ -389,15 +388,17 @@ __global__ __launch_bounds__(wide::kThreads) void attn_relpos_wide_kernel(const 
 template <typename T, int HDP, int VK, bool POS>
 static hipError_t launch_wide(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                               int hd, int h, int w, float scale, hipStream_t stream) {
-  auto kern = attn_relpos_wide_kernel<T, HDP, VK, POS>;
-  constexpr size_t lds = wide::lds_bytes<T, HDP>();
+  // 8 waves (two per SIMD) where their scratch fits beside the tiles, else 4
+  constexpr int NW = wide::lds_bytes<T, HDP, 8>() <= 160 * 1024 ? 8 : 4;
+  auto kern = attn_relpos_wide_kernel<T, HDP, VK, POS, NW>;
+  constexpr size_t lds = wide::lds_bytes<T, HDP, NW>();
   static_assert(lds <= 160 * 1024, "LDS");
   static std::atomic<unsigned long long> lds_done{0};
   if (const hipError_t e = lds_opt_in(lds_done, (const void*)kern, (int)lds); e != hipSuccess) return e;
   const int n = h * w;
-  const int qblocks = (n + wide::kWaves * 32 - 1) / (wide::kWaves * 32);
+  const int qblocks = (n + NW * 32 - 1) / (NW * 32);
   const long blocks = (long)bh * qblocks;
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(wide::kThreads), lds, stream, (const T*)q, (const T*)kt,
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NW * 64), lds, stream, (const T*)q, (const T*)kt,
                      (const T*)v, (const T*)table, (T*)out, hd, h, w, scale, qblocks);
   return hipGetLastError();
 }
