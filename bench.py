@@ -320,6 +320,27 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
         res[f"vit_h_{name}_layer_bf16"] = leg
         del qb, ktb, vb, ob
 
+    # A global layer past the 64 x 64 grid: ViT-H at a 1536 x 1536 input (96 x 96 tokens, 16 heads x 80),
+    # f16. The reference's own GPU sequence stops at 8192 keys (its relpos_softmax limit); the fused
+    # kernel walks the 96 columns in two 64-column passes.
+    side = 96
+    n = side * side
+    qw = torch.randn(HEADS, n, HD, device=dev, generator=g).half()
+    ktw = torch.randn(HEADS, HD, n, device=dev, generator=g).half()
+    vw = torch.randn(HEADS, n, HD, device=dev, generator=g).half()
+    tw = (0.02 * torch.randn(4 * side - 2, HD, device=dev, generator=g)).half()
+    ow = torch.empty_like(qw)
+    ms = timer.avg_ms(lambda: check(lib, lib.sam_hip_attn_relpos(qw.data_ptr(), ktw.data_ptr(), vw.data_ptr(),
+                                                                  tw.data_ptr(), ow.data_ptr(), 1, HEADS, side, side,
+                                                                  HD, HD ** -0.5, sp)), 10)
+    f = flops(HEADS, n)
+    res["vit_h_global_layer_96x96_f16"] = {
+        "workload": f"SAM ViT-H global attention layer at a 1536x1536 input, f16: {HEADS} x {side}x{side}, hd {HD} "
+                    "(past the reference GPU path's 8192-key limit)",
+        "us": round(ms * 1e3, 2), "tflops": round(f / (ms * 1e-3) / 1e12, 1),
+        "frac_of_f16_mfma_peak": round(f / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f16"], 4)}
+    del qw, ktw, vw, ow
+
     # Platform references for the MFMA roofline, on this GPU in this run: torch's own flash attention
     # (scaled_dot_product_attention, no bias) at the ViT-H global layer's shape, and a plain hipBLASLt f16
     # GEMM through torch. Neither is part of the path; they show what the platform's own kernels reach
