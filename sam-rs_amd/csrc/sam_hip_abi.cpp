@@ -121,6 +121,8 @@ int sam_hip_attn_relpos(const void* q, const void* kt, const void* v, const void
   if (h > 128 || w > 128 || (dtype == 0 && (h > 64 || w > 64)))
     return fail(SAM_HIP_EUNSUPPORTED, "attn-relpos: the fused kernels support grids up to %s, got %dx%d",
                 dtype == 0 ? "64x64 in f32" : "128x128", h, w);
+  if ((long)bh * h * w >= (1L << 31))  // the launch grids count workgroups of 32 to 256 queries in 32 bits
+    return fail(SAM_HIP_EUNSUPPORTED, "attn-relpos: bh*h*w = %ld queries is beyond 2^31", (long)bh * h * w);
   const int align = dtype == 0 ? 4 : 8;
   if (hd % align != 0 || hd > 128)
     return fail(SAM_HIP_EUNSUPPORTED, "attn-relpos: head dim must be a multiple of %d and at most 128, got %d", align,

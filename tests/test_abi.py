@@ -49,6 +49,8 @@ def test_null_pointers_and_bad_sizes_fail_without_a_launch(lib):
     assert b"dtype" in lib.sam_hip_last_error()
     assert lib.sam_hip_attn_relpos(fake, fake, fake, fake, fake, 1, 1, 129, 3, 8, 0.3, None) == 3
     assert lib.sam_hip_attn_relpos(fake, fake, fake, fake, fake, 0, 1, 65, 3, 8, 0.3, None) == 3  # f32 past 64
+    assert lib.sam_hip_attn_relpos(fake, fake, fake, fake, fake, 1, 1 << 20, 64, 64, 8, 0.3, None) == 3
+    assert b"beyond 2^31" in lib.sam_hip_last_error()
     assert lib.sam_hip_attn_relpos(fake, fake, fake, fake, fake, 1, 1, 2, 3, 12, 0.3, None) == 3
     lib.sam_hip_deform_attn.argtypes = [vp] * 4 + [i] * 8 + [ctypes.POINTER(ctypes.c_int), vp]
     shapes = (ctypes.c_int * 10)(*([2, 3] * 5))
