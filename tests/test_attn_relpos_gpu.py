@@ -215,6 +215,36 @@ def test_global_kernel_many_heads(hip, hd, bh, dtype):
     check_units(hip, tensors, heads, h, w, dtype, f"global kernel hd={hd} bh={bh} {dtype}")
 
 
+# Padding keys (grid columns past W, rows past H, the slots of the last key tile) make the kernels'
+# tile loads reach past the last unit's kT and V; the loads go through buffer descriptors of the unit
+# (window kernels) or stay inside the tensor, so nothing past the end may reach a result. kT and v
+# here are views of buffers whose tails hold NaN: a load past the end that was not zeroed would put NaN
+# into S or into P.V (0 * NaN). The last units of every kernel family are checked against the oracle.
+PAST_END = [(14, 14, 80), (13, 12, 80), (14, 14, 64), (15, 8, 64), (7, 11, 80), (37, 64, 80), (65, 64, 64)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("h,w,hd", PAST_END)
+def test_loads_past_the_last_unit_read_no_data(hip, h, w, hd, dtype):
+    bh = 6
+    n = h * w
+    print(f"past-end {dtype} h={h} w={w} hd={hd}", flush=True)
+    arrays = make_inputs(h, w, bh, hd, 900 + n + hd, dtype)
+    q, kt, v, table = (to_dev(a, dtype) for a in arrays)
+    tail = 64 * 1024  # elements of NaN after each tensor
+    def nan_tailed(x):
+        buf = torch.full((x.numel() + tail,), float("nan"), device="cuda", dtype=x.dtype)
+        buf[: x.numel()].copy_(x.reshape(-1))
+        return buf[: x.numel()].view(x.shape)
+    kt2, v2 = nan_tailed(kt), nan_tailed(v)
+    got = hip.attention_relpos(q, kt2, v2, table, h, w, hd ** -0.5)
+    torch.cuda.synchronize()
+    got = got.float().cpu().numpy()
+    assert np.isfinite(got).all(), "a load past the end reached the output"
+    want = oracle.attention_relpos(*arrays, h, w, hd ** -0.5)
+    check(got, want, dtype, f"past-end {h}x{w} hd={hd} {dtype}")
+
+
 def test_window_kernel_units_are_independent(hip):
     """At 1600 units the windowed kernel's workgroups run several half units each: permuting the units
     moves them to other workgroups and pipeline positions, and the output rows move with them exactly."""
