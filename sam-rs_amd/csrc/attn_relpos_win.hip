@@ -116,13 +116,16 @@ __device__ __forceinline__ int win_xcd_block(int i, int total) {
   return x * per + (x < rem ? x : rem) + j;
 }
 
-template <typename T, int HD>
+// HW > 0: the grid is HW x HW, a compile-time constant (the SAM windows, 14 x 14), so that the index
+// arithmetic of the DMAs, the bias scatter and the stores folds; HW == 0 takes H and W at run time.
+template <typename T, int HD, int HW>
 __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const T* __restrict__ q,
                                                                        const T* __restrict__ kt,
                                                                        const T* __restrict__ v,
                                                                        const T* __restrict__ table,
-                                                                       T* __restrict__ out, int H, int W,
+                                                                       T* __restrict__ out, int H_, int W_,
                                                                        float scale, int nunits, int n8) {
+  const int H = HW ? HW : H_, W = HW ? HW : W_;
   using namespace win;
   typedef Shape<HD> S;
   constexpr int kKS = S::kKS, kMBO = S::kMBO, kBuf = S::kBuf, kTDma = S::kTDma;
@@ -490,9 +493,11 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
 template <typename T, int HD>
 static hipError_t launch_win(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                              int h, int w, float scale, hipStream_t stream) {
-  auto kern = attn_relpos_win_kernel<T, HD>;
+  const bool sam = h == 14 && w == 14;
+  auto kern = sam ? attn_relpos_win_kernel<T, HD, 14> : attn_relpos_win_kernel<T, HD, 0>;
   constexpr size_t lds = win::Shape<HD>::kLdsBytes;
-  static std::atomic<unsigned long long> lds_done{0};
+  static std::atomic<unsigned long long> lds_done_all[2];
+  std::atomic<unsigned long long>& lds_done = lds_done_all[sam];
   if (const hipError_t e = lds_opt_in(lds_done, (const void*)kern, (int)lds); e != hipSuccess) return e;
   // When the grid fits in two rounds of the chip's workgroup slots, the second round should hold the
   // lighter second halves (68 of 196 queries at 14x14), so all first halves go first. Larger grids
