@@ -66,8 +66,11 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c0, float s0
   y1 = x1 * c1 + x0 * s1;
 }
 
+// f16 4-wave workgroups (head dims up to 64) are held to 168 registers, so that three share a CU (bf16,
+// whose P.V takes P as hi + lo, would spill there and runs two to a CU).
 template <typename T, int DP, int NW, bool ROPEQ, bool MASK>
-__global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
+__global__ __launch_bounds__(NW * 64, NW == 4 && DP <= 64 && __is_same(T, f16) ? 3 : 1) void flash_fwd_kernel(
+    FlashParams p) {
   typedef FlashGeom<T, DP, NW> FG;
   typedef typename Vec<T>::x8 X8;
   constexpr bool kSplitP = __is_same(T, bf16);
@@ -485,25 +488,45 @@ static hipError_t launch_flash(FlashParams p, bool ropeq, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Waves per workgroup of the f16 / bf16 kernel. Up to head dim 64 a wave needs 161-176 registers, so
+// two 8-wave workgroups (four waves per SIMD) would not fit a CU and an 8-wave workgroup runs alone on
+// it; 4-wave workgroups run two or three to a CU, each on its own barrier schedule. Head dims 96 and
+// 128 need 221-240 registers, two waves per SIMD either way, and keep 8 waves (each K/V tile serves
+// twice the queries); head dim 256 takes 4.
 template <int DP>
 constexpr int flash_waves() {
-  return DP <= 128 ? 8 : 4;
+  return DP <= 64 ? 4 : DP <= 128 ? 8 : 4;
 }
 
 int flash_padded_dim(int d) { return d <= 32 ? 32 : d <= 64 ? 64 : d <= 96 ? 96 : d <= 128 ? 128 : 256; }
 
-int flash_queries_per_block(int d) { return 32 * (flash_padded_dim(d) <= 128 ? 8 : 4); }
+// Queries per workgroup: 32 per wave (the f32 kernel keeps 8 waves up to head dim 128).
+int flash_queries_per_block(int dtype, int d) {
+  const int dp = flash_padded_dim(d);
+  if (dtype == kF32) return 32 * (dp <= 128 ? 8 : 4);
+  return 32 * (dp <= 64 ? 4 : dp <= 128 ? 8 : 4);
+}
 
-// Key splits: enough workgroups to give every CU its resident share (one workgroup per CU at head dim
-// 256, two below), at least 2 key tiles per split.
-void flash_plan(int b, int h, int lq, int lk, int d, int cus, int* qblocks, int* nsplit, int* tps) {
-  const int qpb = flash_queries_per_block(d);
+// Key splits, at least 2 key tiles per split. Head dims above 64 (and f32): enough workgroups to give
+// every CU its resident share (one workgroup per CU at head dim 256, two below). f16 / bf16 up to head
+// dim 64 (4-wave workgroups, three (f16) or two (bf16) resident per CU): as many splits as still fit
+// one round of resident workgroups, none once the query blocks alone fill it. Measured on f16 against
+// other split counts: a short key range (SAM 3's 576-token windows) loses 35% when split in two, and
+// 4096 x 4096 over 16 heads 9%, while 12 heads (384 query blocks) gain 13% from two splits.
+void flash_plan(int dtype, int b, int h, int lq, int lk, int d, int cus, int* qblocks, int* nsplit, int* tps) {
+  const int qpb = flash_queries_per_block(dtype, d);
   *qblocks = (lq + qpb - 1) / qpb;
   const int tiles = (lk + 63) / 64;
   const long base = (long)b * h * *qblocks;
-  const long target = (long)cus * (flash_padded_dim(d) <= 128 ? 2 : 1);
+  const int dp = flash_padded_dim(d);
   int ns = 1;
-  if (base < target) ns = (int)((target + base - 1) / base);
+  if (dtype != kF32 && dp <= 64) {
+    const long slots = (long)cus * (dtype == kF16 ? 3 : 2);
+    if (base < slots) ns = (int)(slots / base);
+  } else {
+    const long target = (long)cus * (dp <= 128 ? 2 : 1);
+    if (base < target) ns = (int)((target + base - 1) / base);
+  }
   const int maxs = tiles / 2 > 1 ? tiles / 2 : 1;
   if (ns > maxs) ns = maxs;
   if (ns > 64) ns = 64;

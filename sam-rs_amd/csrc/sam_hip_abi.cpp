@@ -386,7 +386,7 @@ FlashPlan plan_flash(int dtype, int b, int lq, int lk, int h, int d, int n_rope_
   FlashPlan pl;
   int cus = device_cus();
   if (cu_cap > 0 && cus > cu_cap) cus = cu_cap;
-  samhip::flash_plan(b, h, lq, lk, d, cus, &pl.qblocks, &pl.nsplit, &pl.tps);
+  samhip::flash_plan(dtype, b, h, lq, lk, d, cus, &pl.qblocks, &pl.nsplit, &pl.tps);
   pl.partial_bytes = round256(samhip::flash_partial_bytes(b, h, lq, d, pl.nsplit));
   const size_t elem = dtype == 0 ? 4 : 2;
   pl.krot_bytes = n_rope_k > 0 ? round256((size_t)b * lk * h * d * elem) : 0;

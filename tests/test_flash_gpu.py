@@ -35,10 +35,13 @@ def rounded(r, shape, dtype, std=1.0):
 
 # (b, lq, lk, h, d): tiny and ragged shapes (partial key tiles, partial query blocks, one key), the
 # head dims of the reference's callers (Hiera 96 at its widest stage, SAM 3 ViT 64, memory attention
-# 256), and shapes whose few query blocks force the key-split path.
+# 256), and shapes whose few query blocks force the key-split path. Up to head dim 64 a workgroup holds
+# 128 queries: several query blocks with a partial last one (576 queries: 4.5 blocks, two idle waves),
+# with and without key splits.
 BLHD = [(1, 5, 7, 2, 16), (2, 33, 65, 3, 64), (1, 40, 100, 1, 256), (2, 130, 200, 4, 96), (1, 64, 64, 8, 64),
         (1, 300, 1000, 2, 128), (1, 1, 1, 1, 8), (1, 17, 3000, 1, 64), (3, 49, 49, 2, 32), (1, 257, 129, 1, 256),
-        (2, 130, 517, 3, 256), (1, 70, 33, 2, 256), (1, 128, 64, 1, 256)]
+        (2, 130, 517, 3, 256), (1, 70, 33, 2, 256), (1, 128, 64, 1, 256), (2, 576, 576, 3, 64),
+        (1, 1000, 1000, 2, 64), (1, 300, 700, 2, 32)]
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
@@ -50,6 +53,30 @@ def test_flash_attn_matches_oracle(hip, b, lq, lk, h, d, dtype):
     torch.cuda.synchronize()
     want = oracle.mha_blhd(q, k, v)
     check(got.float().cpu().numpy(), want, dtype, f"flash_attn b{b} lq{lq} lk{lk} h{h} d{d} {dtype}")
+
+
+# SAM 3 ViT's own attention calls (sam3/vision.rs:113-121), full size: the 24 x 24 windows of a 72 x 72
+# grid (9 windows of 576 tokens) and the global grid (5184 tokens), 16 heads of 64. The GPU runs every
+# window and head; the oracle checks two windows and two heads.
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("case", ["window", "global"])
+def test_sam3_vit_attention_full_size(hip, case, dtype):
+    b, l = (9, 576) if case == "window" else (1, 5184)
+    h, d = 16, 64
+    print(f"sam3 vit {case} {dtype}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(31 if case == "window" else 32)
+    q, k, v = (torch.randn(b, l, h, d, device="cuda", generator=g).to(TORCH_DT[dtype]) for _ in range(3))
+    got = hip.flash_attn(q, k, v)
+    torch.cuda.synchronize()
+    host = lambda t: t.float().cpu().numpy()
+    if case == "window":
+        sel = [0, 8]
+        want = oracle.mha_blhd(host(q[sel]), host(k[sel]), host(v[sel]))
+        check(host(got[sel]), want, dtype, f"sam3 vit window {dtype}")
+    else:
+        sel = [0, 15]
+        want = oracle.mha_blhd(host(q[:, :, sel]), host(k[:, :, sel]), host(v[:, :, sel]))
+        check(host(got[:, :, sel]), want, dtype, f"sam3 vit global {dtype}")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
