@@ -292,6 +292,54 @@ def secondary(torch, sam_hip, lib, dev, sp, timer, cpu=True):
             "scaled by 4 layers")
     del layers, ws
 
+    # SAM 3 ViT image-encoder attention (sam3/vision.rs:96-121) at a 1008 x 1008 input, batch 1, f16: 72 x 72
+    # tokens, 16 heads x 64, 32 layers of which 4 global (5184 tokens) and 28 windowed (9 windows of 24 x
+    # 24 = 576 tokens); the flash attention the reference reaches through candle_flash_attn, each layer
+    # on its own operands (q, k, v as the [nw, n, H, D] slices of the packed qkv_rope output).
+    s3 = []
+    for i in range(32):
+        glob_layer = i in (7, 15, 23, 31)
+        nw, n = (1, 5184) if glob_layer else (9, 576)
+        qkv = torch.randn(3, nw, n, 16, 64, device=dev, generator=g).half()
+        s3.append((nw, n, qkv, torch.empty(nw, n, 16, 64, device=dev, dtype=torch.float16)))
+    s3ws = max(lib.sam_hip_flash_attn_workspace_size(1, nw_, n_, n_, 16, 64, 0) for nw_, n_, _, _ in s3[6:8])
+    s3buf = torch.empty(max(s3ws, 1), dtype=torch.uint8, device=dev)
+
+    def s3_call(L):
+        nw, n, qkv, out = L
+        check(lib, lib.sam_hip_flash_attn(qkv[0].data_ptr(), qkv[1].data_ptr(), qkv[2].data_ptr(), out.data_ptr(), 1,
+                                          nw, n, n, 16, 64, None, None, None, None, 0.125, None, None, 0, 0, 0,
+                                          vp(s3buf.data_ptr()), s3buf.numel(), sp))
+
+    s3_ms = timer.avg_ms(lambda: [s3_call(L) for L in s3], 10, warm_s=0.1)
+    s3w_ms = timer.avg_ms(lambda: [s3_call(L) for L in s3 if L[0] == 9], 10)
+    s3g_ms = (s3_ms - s3w_ms) / 4
+    f_w, f_g = 4.0 * 9 * 16 * 576 * 576 * 64, 4.0 * 16 * 5184 * 5184 * 64
+    s3_fl = 28 * f_w + 4 * f_g
+    res["sam3_vit_attention_f16"] = {
+        "workload": "SAM 3 ViT image-encoder attention, 1008x1008 input, batch 1: 28 windowed layers (9 x 576 tokens) "
+                    "+ 4 global layers (5184 tokens), 16 heads x 64, f16 flash attention",
+        "ms_per_image": round(s3_ms, 4), "window_layer_us": round(s3w_ms / 28 * 1e3, 2),
+        "global_layer_us": round(s3g_ms * 1e3, 2),
+        "tflops": round(s3_fl / (s3_ms * 1e-3) / 1e12, 1),
+        "frac_of_f16_mfma_peak": round(s3_fl / (s3_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f16"], 4),
+        "global_frac_of_f16_mfma_peak": round(f_g / (s3g_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f16"], 4),
+    }
+    if cpu and orc.bf16_available():
+        # the reference's CPU flash attention (cpu_gemm.rs:361-417, bf16 on AVX-512 BF16 hosts): one window
+        # (16 heads) of a windowed layer and 2 of the 16 heads of a global layer, scaled to the image
+        _, _, qkv_w, _ = s3[0]
+        _, _, qkv_g, _ = s3[7]
+        qw_, kw_, vw_ = (host(qkv_w[j, :1]) for j in range(3))
+        qg_, kg_, vg_ = (host(qkv_g[j][:, :, :2]).copy() for j in range(3))
+        tw_ = best_of(lambda: orc.bf16_flash_attention(qw_, kw_, vw_, nthreads=cores), 1)
+        tg_ = best_of(lambda: orc.bf16_flash_attention(qg_, kg_, vg_, nthreads=cores), 1)
+        res["sam3_vit_attention_f16"]["cpu_baseline"] = cpu_leg(
+            tw_ * 9 * 28 + tg_ * 8 * 4, 1, 1e3, "ms/image",
+            f"bf16 branch of the reference's CPU flash attention: one window of a windowed layer ({tw_:.3f} s, "
+            f"x 9 windows x 28 layers) and 2 of 16 heads of a global layer ({tg_:.3f} s, x 8 x 4 layers)")
+    del s3, s3buf
+
     # The ViT-H attention layers of the headline in bf16 (batch 1): the global layer (16 heads x 64x64) on
     # the bf16 MFMA, and a windowed layer (400 units x 14x14), each on fresh operand sets so that every
     # call reads its inputs from HBM, as the headline's layers do.
