@@ -155,13 +155,26 @@ __global__ __launch_bounds__(NW * 64, NW == 4 && DP <= 64 && __is_same(T, f16) ?
     }
   };
 
-  // first tiles in flight before Q is fetched
+  // The first K and V tiles, the second K tile (in a register set of its own) and the Q fragments are
+  // all in flight together, so that the key loop starts one memory latency after the workgroup does
+  // (a short key range, such as Hiera's or SAM 3's windows, is mostly this prologue).
   const int tl = t_end - 1;
   load_k(t_begin);
   load_v(t_begin);
-  store_k(0);
-  store_v(0);
-  load_k(min(t_begin + 1, tl));
+  u32x4 kreg1[PT];
+  bool kok1[PT];
+  {
+    const int t1 = min(t_begin + 1, tl);
+#pragma unroll
+    for (int u = 0; u < PT; ++u) {
+      const int c = tid + u * NT;
+      const int r = c / CPR, c8 = (c % CPR) * 8;
+      const int key = (t1 << 6) + r;
+      const bool ok = (CH % NT == 0 || c < CH) && key < kend && c8 < d;
+      kok1[u] = ok;
+      kreg1[u] = *reinterpret_cast<const u32x4*>(kbase + (ok ? (long)key * p.sk[1] + c8 : 0));
+    }
+  }
 
   // Q fragments (B operand of S^T = K Q^T): lane supplies Q[query n][16*s + 8*hh + j], j = 0..7
   X8 qf[KS];
@@ -188,7 +201,17 @@ __global__ __launch_bounds__(NW * 64, NW == 4 && DP <= 64 && __is_same(T, f16) ?
     }
     qf[s] = val;
   }
-  store_k(1);
+  store_k(0);
+  store_v(0);
+  {
+    T* kb = ks_base + KBUF;
+#pragma unroll
+    for (int u = 0; u < PT; ++u) {
+      const int c = tid + u * NT;
+      if (CH % NT == 0 || c < CH)
+        *reinterpret_cast<u32x4*>(kb + (c / CPR) * KSTR + (c % CPR) * 8) = kok1[u] ? kreg1[u] : u32x4{};
+    }
+  }
   __syncthreads();
 
   // per-lane constant parts of the LDS addresses
