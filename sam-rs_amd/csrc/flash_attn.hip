@@ -514,37 +514,35 @@ static hipError_t launch_flash(FlashParams p, bool ropeq, hipStream_t stream) {
 // Waves per workgroup of the f16 / bf16 kernel. Up to head dim 64 a wave needs 161-176 registers, so
 // two 8-wave workgroups (four waves per SIMD) would not fit a CU and an 8-wave workgroup runs alone on
 // it; 4-wave workgroups run two or three to a CU, each on its own barrier schedule. Head dims 96 and
-// 128 need 221-240 registers, two waves per SIMD either way, and keep 8 waves (each K/V tile serves
-// twice the queries); head dim 256 takes 4.
-template <int DP>
-constexpr int flash_waves() {
-  return DP <= 64 ? 4 : DP <= 128 ? 8 : 4;
-}
-
+// 128 need 221-240 registers, two waves per SIMD either way: 8 waves (each K/V tile serves twice the
+// queries) for key ranges past 16 tiles, 4 for shorter ones (Hiera's windows at head dim 72), where
+// the query blocks of 256 leave CUs idle or padded (measured: 196 x 196 windows 32.3 -> 23.1 us with 4,
+// 4096 x 4096 over 16 heads at 128 179 -> 220 us). Head dim 256 takes 4.
 int flash_padded_dim(int d) { return d <= 32 ? 32 : d <= 64 ? 64 : d <= 96 ? 96 : d <= 128 ? 128 : 256; }
 
 // Queries per workgroup: 32 per wave (the f32 kernel keeps 8 waves up to head dim 128).
-int flash_queries_per_block(int dtype, int d) {
+int flash_queries_per_block(int dtype, int d, int lk) {
   const int dp = flash_padded_dim(d);
   if (dtype == kF32) return 32 * (dp <= 128 ? 8 : 4);
-  return 32 * (dp <= 64 ? 4 : dp <= 128 ? 8 : 4);
+  return 32 * (dp <= 64 ? 4 : dp <= 128 ? (lk <= 16 * 64 ? 4 : 8) : 4);
 }
 
-// Key splits, at least 2 key tiles per split. Head dims above 64 (and f32): enough workgroups to give
-// every CU its resident share (one workgroup per CU at head dim 256, two below). f16 / bf16 up to head
-// dim 64 (4-wave workgroups, three (f16) or two (bf16) resident per CU): as many splits as still fit
-// one round of resident workgroups, none once the query blocks alone fill it. Measured on f16 against
-// other split counts: a short key range (SAM 3's 576-token windows) loses 35% when split in two, and
-// 4096 x 4096 over 16 heads 9%, while 12 heads (384 query blocks) gain 13% from two splits.
+// Key splits, at least 2 key tiles per split. 4-wave f16 / bf16 workgroups (three resident per CU in
+// f16 up to head dim 64, two otherwise): as many splits as still fit one round of resident workgroups,
+// none once the query blocks alone fill it. Measured on f16 against other split counts: a short key
+// range (SAM 3's 576-token windows) loses 35% when split in two, and 4096 x 4096 over 16 heads 9%,
+// while 12 heads (384 query blocks) gain 13% from two splits. Otherwise (8 waves, f32, head dim 256):
+// enough workgroups to give every CU its resident share (one workgroup per CU at head dim 256, two
+// below).
 void flash_plan(int dtype, int b, int h, int lq, int lk, int d, int cus, int* qblocks, int* nsplit, int* tps) {
-  const int qpb = flash_queries_per_block(dtype, d);
+  const int qpb = flash_queries_per_block(dtype, d, lk);
   *qblocks = (lq + qpb - 1) / qpb;
   const int tiles = (lk + 63) / 64;
   const long base = (long)b * h * *qblocks;
   const int dp = flash_padded_dim(d);
   int ns = 1;
-  if (dtype != kF32 && dp <= 64) {
-    const long slots = (long)cus * (dtype == kF16 ? 3 : 2);
+  if (dtype != kF32 && dp <= 128 && qpb == 128) {
+    const long slots = (long)cus * (dtype == kF16 && dp <= 64 ? 3 : 2);
     if (base < slots) ns = (int)(slots / base);
   } else {
     const long target = (long)cus * (dp <= 128 ? 2 : 1);
@@ -563,14 +561,16 @@ size_t flash_partial_bytes(int b, int h, int lq, int d, int nsplit) {
   return (size_t)nsplit * b * h * lq * (flash_padded_dim(d) + 2) * sizeof(float);
 }
 
+// The waves of the plan's query blocks (flash_queries_per_block) pick the instance.
 template <typename T>
 static hipError_t flash_dispatch(FlashParams p, bool ropeq, hipStream_t s) {
+  const bool four = flash_queries_per_block(__is_same(T, f16) ? kF16 : kBF16, p.d, p.lk) == 128;
   switch (flash_padded_dim(p.d)) {
-    case 32: return launch_flash<T, 32, flash_waves<32>()>(p, ropeq, s);
-    case 64: return launch_flash<T, 64, flash_waves<64>()>(p, ropeq, s);
-    case 96: return launch_flash<T, 96, flash_waves<96>()>(p, ropeq, s);
-    case 128: return launch_flash<T, 128, flash_waves<128>()>(p, ropeq, s);
-    default: return launch_flash<T, 256, flash_waves<256>()>(p, ropeq, s);
+    case 32: return launch_flash<T, 32, 4>(p, ropeq, s);
+    case 64: return launch_flash<T, 64, 4>(p, ropeq, s);
+    case 96: return four ? launch_flash<T, 96, 4>(p, ropeq, s) : launch_flash<T, 96, 8>(p, ropeq, s);
+    case 128: return four ? launch_flash<T, 128, 4>(p, ropeq, s) : launch_flash<T, 128, 8>(p, ropeq, s);
+    default: return launch_flash<T, 256, 4>(p, ropeq, s);
   }
 }
 

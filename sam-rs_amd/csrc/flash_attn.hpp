@@ -38,7 +38,7 @@ long flash256_vt_blocks(const VtJob& j);                                // workg
 hipError_t flash256_vt(const VtJob& j, hipStream_t stream);             // the pass as a launch of its own
 
 int flash_padded_dim(int d);
-int flash_queries_per_block(int dtype, int d);
+int flash_queries_per_block(int dtype, int d, int lk);
 void flash_plan(int dtype, int b, int h, int lq, int lk, int d, int cus, int* qblocks, int* nsplit, int* tps);
 size_t flash_partial_bytes(int b, int h, int lq, int d, int nsplit);
 hipError_t flash_attn_half(int dtype, FlashParams p, bool ropeq, hipStream_t stream);

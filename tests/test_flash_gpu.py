@@ -35,13 +35,14 @@ def rounded(r, shape, dtype, std=1.0):
 
 # (b, lq, lk, h, d): tiny and ragged shapes (partial key tiles, partial query blocks, one key), the
 # head dims of the reference's callers (Hiera 96 at its widest stage, SAM 3 ViT 64, memory attention
-# 256), and shapes whose few query blocks force the key-split path. Up to head dim 64 a workgroup holds
-# 128 queries: several query blocks with a partial last one (576 queries: 4.5 blocks, two idle waves),
-# with and without key splits.
+# 256), and shapes whose few query blocks force the key-split path. Up to head dim 64, and at 96 and 128
+# for up to 1024 keys, a workgroup holds 128 queries (256 past that): several query blocks with a
+# partial last one (576 queries: 4.5 blocks, two idle waves), with and without key splits, and both
+# sides of the 1024-key line.
 BLHD = [(1, 5, 7, 2, 16), (2, 33, 65, 3, 64), (1, 40, 100, 1, 256), (2, 130, 200, 4, 96), (1, 64, 64, 8, 64),
         (1, 300, 1000, 2, 128), (1, 1, 1, 1, 8), (1, 17, 3000, 1, 64), (3, 49, 49, 2, 32), (1, 257, 129, 1, 256),
         (2, 130, 517, 3, 256), (1, 70, 33, 2, 256), (1, 128, 64, 1, 256), (2, 576, 576, 3, 64),
-        (1, 1000, 1000, 2, 64), (1, 300, 700, 2, 32)]
+        (1, 1000, 1000, 2, 64), (1, 300, 700, 2, 32), (1, 260, 1100, 2, 96), (2, 300, 1024, 1, 128)]
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
