@@ -364,8 +364,8 @@ __global__ __launch_bounds__(NWV * 64) void attn_relpos_kernel(const T* __restri
         }
         float mm = s_cur[mb][0];
 #pragma unroll
-        for (int e = 1; e < 16; ++e) mm = fmaxf(mm, s_cur[mb][e]);
-        mt = fmaxf(mt, POS ? fmaf(mm, sc, rh[mb]) : mm + rh[mb]);
+        for (int e = 1; e < 16; ++e) mm = max_nc(mm, s_cur[mb][e]);
+        mt = max_nc(mt, POS ? fmaf(mm, sc, rh[mb]) : mm + rh[mb]);
       }
       mt = max_with_partner32(mt);
       if (wave_any(mt > m_run + kRescaleSlack)) {

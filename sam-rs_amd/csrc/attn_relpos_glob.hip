@@ -328,7 +328,7 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mm = fmaxf(mm, s_cur[mb][e]);
+      for (int e = 0; e < 16; ++e) mm = max_nc(mm, s_cur[mb][e]);
     const float mt = max_with_partner32(kPre ? mm : fmaf(mm, sc, c));
     float cc = c;
     if (wave_any(t == 0 || mt > kSlack)) {

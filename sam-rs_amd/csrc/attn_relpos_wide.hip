@@ -284,8 +284,8 @@ __global__ __launch_bounds__(NW * 64) void attn_relpos_wide_kernel(const T* __re
         }
         float mm = s_cur[mb][0];
 #pragma unroll
-        for (int e = 1; e < 16; ++e) mm = fmaxf(mm, s_cur[mb][e]);
-        mt = fmaxf(mt, POS ? fmaf(mm, sc, rh) : mm + rh);
+        for (int e = 1; e < 16; ++e) mm = max_nc(mm, s_cur[mb][e]);
+        mt = max_nc(mt, POS ? fmaf(mm, sc, rh) : mm + rh);
       }
       mt = max_with_partner32(mt);
       if (wave_any(mt > m_run + kSlack)) {

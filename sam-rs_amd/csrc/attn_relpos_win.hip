@@ -377,8 +377,8 @@ __global__ __launch_bounds__(win::kThreads, 2) void attn_relpos_win_kernel(const
     for (int mb = 0; mb < NB; ++mb) {
       float mm = s[mb][0];
 #pragma unroll
-      for (int e = 1; e < 16; ++e) mm = fmaxf(mm, s[mb][e]);
-      mt = fmaxf(mt, fmaf(mm, sc, rh[t][mb]));
+      for (int e = 1; e < 16; ++e) mm = max_nc(mm, s[mb][e]);
+      mt = max_nc(mt, fmaf(mm, sc, rh[t][mb]));
     }
     mt = max_with_partner32(mt);
     if (wave_any(mt > m_run + kSlack)) {

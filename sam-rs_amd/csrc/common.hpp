@@ -113,11 +113,16 @@ __device__ __forceinline__ typename Vec<T>::x8 join8(i16x4 lo, i16x4 hi) {
   return __builtin_bit_cast(typename Vec<T>::x8, v);
 }
 
+// max(a, b) as v_maximum_f32 / v_maximum3_f32: unlike fmaxf it needs no quieting of its operands
+// first (a NaN operand gives NaN; +0 is above -0), which the max reductions over MFMA results would
+// otherwise pay for with one extra instruction per operand not known to be canonical.
+__device__ __forceinline__ float max_nc(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Value of `x` held by lane (l ^ 32): v_permlane32_swap exchanges the upper half of its first operand
 // with the lower half of its second, so with both operands = x the pair holds x[l] and x[l ^ 32].
 __device__ __forceinline__ float max_with_partner32(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max_nc(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float sum_with_partner32(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -129,7 +134,7 @@ __device__ __forceinline__ float sum_with_partner32(float x) {
 // operands = x the pair holds x[l] and x[l ^ 16]; permlane32_swap then pairs l and l ^ 32.
 __device__ __forceinline__ float max_over_rows16(float x) {
   auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return max_with_partner32(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+  return max_with_partner32(max_nc(__uint_as_float(r[0]), __uint_as_float(r[1])));
 }
 __device__ __forceinline__ float sum_over_rows16(float x) {
   auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);

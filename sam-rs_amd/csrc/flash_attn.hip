@@ -280,7 +280,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 && DP <= 64 && __is_same(T, f16) ?
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) mm = fmaxf(mm, s_cur[mb][e]);
+        for (int e = 0; e < 16; ++e) mm = max_nc(mm, s_cur[mb][e]);
       const float mt = max_with_partner32(MASK ? mm : mm * sc);
       if (wave_any(mt > m_run + kFlashSlack)) {
         const float m_new = fmaxf(m_run, mt);

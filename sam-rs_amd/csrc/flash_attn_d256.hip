@@ -217,7 +217,7 @@ __global__ __launch_bounds__(f256::kThreads) void flash256_kernel(FlashParams p)
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mm = fmaxf(mm, s[kb][i]);
+        for (int i = 0; i < 4; ++i) mm = max_nc(mm, s[kb][i]);
       const float mt = max_over_rows16(mm) * p.sc;
       if (wave_any(mt > m_run + kSlack)) {
         const float m_new = fmaxf(m_run, mt);
