@@ -135,6 +135,8 @@ def _contig(*ts: torch.Tensor):
     for t in ts:
         if not t.is_cuda:
             raise SamHipError("sam-rs HIP kernels need device tensors")
+        if t.device != ts[0].device:
+            raise SamHipError(f"sam-rs HIP kernels need all operands on one device: {t.device} vs {ts[0].device}")
         if not t.is_contiguous():
             raise SamHipError("sam-rs kernels need contiguous inputs")  # kernels.rs:1100
 
@@ -401,6 +403,8 @@ def _flash(q, k, v, out, layout: str, scale: float, cos=None, sin=None, n_rope_q
     for t in (q, k, v, out):
         if not t.is_cuda:
             raise SamHipError("sam-rs HIP kernels need device tensors")
+        if t.device != q.device:
+            raise SamHipError(f"sam-rs HIP kernels need all operands on one device: {t.device} vs {q.device}")
     dt = _dtype(q, k, v)
     if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
         raise SamHipError(f"flash-attn: incompatible q/k/v shapes {tuple(q.shape)}/{tuple(k.shape)}/{tuple(v.shape)}")
@@ -460,6 +464,8 @@ def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask=None) -> torch.
     for t in (q, k, v, mask):
         if not t.is_cuda:
             raise SamHipError("sam-rs HIP kernels need device tensors")
+        if t.device != q.device:
+            raise SamHipError(f"sam-rs HIP kernels need all operands on one device: {t.device} vs {q.device}")
     dt = _dtype(q, k, v)
     if mask.dtype != q.dtype:
         raise SamHipError(f"sdpa: the mask must have q's dtype {q.dtype}, got {mask.dtype}")
