@@ -494,15 +494,18 @@ __global__ __launch_bounds__(rsm::kWaves * 64) void relpos_softmax_scalar_kernel
     for (int k = lane; k < N; k += 64) {
       const int kh = k / W, kw = k - kh * W;
       const float x = (to_f32(srow[k]) * scale + brow[W + kh]) + brow[kw];
+      // a -inf score adds nothing (also while m is still -inf); a NaN score makes the sum NaN, so the
+      // row comes out NaN as the reference's softmax returns it
       if (x > m) {
         sum = sum * exp2_fast((m - x) * kLog2e) + 1.f;
         m = x;
-      } else {
+      } else if (x != -INFINITY) {
         sum += exp2_fast((x - m) * kLog2e);
       }
     }
     const float mw = wave_max64(m);
-    sum = m == -INFINITY ? 0.f : sum * exp2_fast((m - mw) * kLog2e);
+    // a lane with no finite score (m = -inf) holds 0, or NaN after a NaN score
+    sum = m == -INFINITY ? sum : sum * exp2_fast((m - mw) * kLog2e);
     const float inv = 1.f / wave_sum64(sum);
     T* orow = out + (r0 + rl) * (long)N;
     for (int k = lane; k < N; k += 64) {
