@@ -1,0 +1,87 @@
+"""Degenerate shapes on an MI355X: one-token grids, one-key attention, and grids of a single row or
+column, through every dtype.
+
+With one key the softmax weight is exactly 1 (exp(0) / exp(0)), so the reference's sequence
+(bmm -> relpos_softmax -> bmm, sam1/encoder.rs:79-82, kernels.rs:12-43) and its flash attention return
+v itself: these cases are checked bit for bit. Single-row and single-column grids (1 x w, h x 1, up to
+the wide kernel's 128) are checked against the oracle at the usual bars (tests/parity.py).
+"""
+import numpy as np
+import pytest
+import torch
+
+import sam_oracle as oracle
+from parity import check, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import sam_hip
+
+    sam_hip.load()
+    assert torch.cuda.is_available(), "no GPU visible"
+    return sam_hip
+
+
+def draw(r, shape, dtype, std=1.0):
+    return oracle.round_to((std * r.standard_normal(shape)).astype(np.float32), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("hd", [16, 64, 80])
+def test_one_token_grid_returns_v(hip, hd, dtype):
+    print(f"one-token grid {dtype} hd={hd}", flush=True)
+    r = np.random.default_rng(7400 + hd)
+    bh = 5
+    q, kt, v = draw(r, (bh, 1, hd), dtype), draw(r, (bh, hd, 1), dtype), draw(r, (bh, 1, hd), dtype)
+    table = draw(r, (2, hd), dtype, 0.02)
+    got = hip.attention_relpos(to_dev(q, dtype), to_dev(kt, dtype), to_dev(v, dtype), to_dev(table, dtype), 1, 1,
+                               hd ** -0.5)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.float().cpu().numpy(), v)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+def test_one_token_relpos_softmax_is_one(hip, dtype):
+    r = np.random.default_rng(7410)
+    s, q, t = draw(r, (3, 1, 1), dtype), draw(r, (3, 1, 64), dtype), draw(r, (2, 64), dtype)
+    got = hip.relpos_softmax(to_dev(s, dtype), to_dev(q, dtype), to_dev(t, dtype), 1, 1, 0.125)
+    torch.cuda.synchronize()
+    assert (got.float().cpu().numpy() == 1.0).all()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("lq,h,d", [(1, 1, 64), (300, 2, 64), (70, 3, 96), (33, 1, 256)])
+def test_one_key_attention_returns_v(hip, lq, h, d, dtype):
+    print(f"one-key flash {dtype} lq={lq} h={h} d={d}", flush=True)
+    r = np.random.default_rng(7420 + lq + d)
+    q, k, v = draw(r, (2, lq, h, d), dtype), draw(r, (2, 1, h, d), dtype), draw(r, (2, 1, h, d), dtype)
+    got = hip.flash_attn(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype))
+    torch.cuda.synchronize()
+    assert np.array_equal(got.float().cpu().numpy(), np.broadcast_to(v, (2, lq, h, d)))
+
+
+# single-row and single-column grids: the generic kernel's shortest rows and columns, a 64-column row
+# (the global kernel's width), and the wide kernel's 128 x 1 and 1 x 128
+LINES = [(1, 2, 64), (2, 1, 64), (1, 64, 80), (64, 1, 80), (1, 64, 64), (64, 1, 64), (1, 128, 64), (128, 1, 64),
+         (1, 100, 80), (100, 1, 80)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("h,w,hd", LINES)
+def test_single_row_and_column_grids(hip, h, w, hd, dtype):
+    if dtype == "f32" and max(h, w) > 64:
+        pytest.skip("f32 rel-pos attention stops at 64 x 64 (larger f32 grids take the reference's sequence)")
+    n = h * w
+    print(f"line grid {dtype} h={h} w={w} hd={hd}", flush=True)
+    r = np.random.default_rng(7430 + 7 * h + w + hd)
+    bh = 3
+    q, kt, v = draw(r, (bh, n, hd), dtype), draw(r, (bh, hd, n), dtype), draw(r, (bh, n, hd), dtype)
+    table = draw(r, (2 * h - 1 + 2 * w - 1, hd), dtype, 0.02)
+    got = hip.attention_relpos(to_dev(q, dtype), to_dev(kt, dtype), to_dev(v, dtype), to_dev(table, dtype), h, w,
+                               hd ** -0.5)
+    torch.cuda.synchronize()
+    want = oracle.attention_relpos(q, kt, v, table, h, w, hd ** -0.5)
+    check(got.float().cpu().numpy(), want, dtype, f"line grid {h}x{w} hd={hd} {dtype}")
