@@ -7,8 +7,11 @@ fused rel-pos attention kernel on inputs already resident in HBM (fresh q/kT/v p
 
 Prints one JSON line: ms per image, the global-layer kernel's achieved TFLOP/s against the f16 MFMA
 peak (timed live with HIP events on the launch stream), and the CPU oracle timed on this host. A
-"secondary" object times the other kernels of the path at their workload shapes: SAM 2.1 memory
-attention (4 layers, f16), Grounding DINO-tiny deformable attention (f32) and the ViT-B f32 layers.
+"secondary" object times the other kernels of the path at their workload shapes: the SAM encoder
+attention sweep (ViT-B/L/H, batch 1/4/8), the ViT-B f32 layers, the ViT-H layers in bf16, SAM 3 ViT's
+flash attention, SAM 2.1 memory attention (4 layers, f16), Grounding DINO-tiny deformable attention
+(f32), relpos_softmax, qkv_split, qkv_rope, the bias ops, preprocessing, the image-encoder forwards,
+and the platform's own GEMM and flash attention as references.
 
     python bench.py [--steps K] [--warmup W] [--batch B] [--dtype f16|bf16] [--no-cpu-baseline]
                     [--no-secondary] [--layers all|global|window] [--copy-probe]
