@@ -13,11 +13,14 @@
 // On gfx950 the MFMA and the VALU work of a SIMD barely overlap (measured: the time of a loop is close
 // to the sum of its MFMA and VALU times), and exp2 issues at a quarter of the FMA rate, so the kernel
 // keeps the per-score VALU work to exp2, the tile max and the f32 -> f16 packing:
-//   * f16: q is pre-scaled by scale*log2(e) and rounded to f16 once (an error below the f16 rounding
-//     of the reference's own bmm(q, kT) output); the MFMA starts from Rw*log2(e) and takes the
-//     per-query term Rh - m_run as one extra k-step (a ones column of K against its f16 hi/lo split),
-//     so the accumulator is the exp2 argument itself. bf16 keeps q exact and applies scale and
-//     Rh - m_run with one fma per score (its 8-bit mantissa would not absorb the pre-scaling).
+//   * f16 at scales up to hd^-1/2 (the model's own): q is pre-scaled by scale*log2(e) and rounded to
+//     f16 once; the MFMA starts from Rw*log2(e) and takes the per-query term Rh - m_run as one extra
+//     k-step (a ones column of K against its f16 hi/lo split), so the accumulator is the exp2 argument
+//     itself. The rounding moves a logit by about 2^-12 of |scale * q . k|: at hd^-1/2 that is the
+//     size of the f16 rounding of the reference's own bmm(q, kT) scores, but it grows with the scale
+//     (scale 1 on N(0, 1) inputs: 8.5e-3 beyond the output's rounding). Larger scales, and bf16 (whose
+//     8-bit mantissa would not absorb the pre-scaling), keep q exact and apply scale and Rh - m_run
+//     with one fma per score (2.5% more time on the ViT-H global layer in f16).
 //   * hd 80: the softmax denominator comes out of the P.V product: the V^T rows 80..95 of the third
 //     32-row block read a ones vector, so O^T rows 80..95 are the running sums of P (as rounded for the
 //     MFMA). hd 64 has no spare rows (two full blocks), so a lane sums its P values on the VALU (v_dot2
@@ -77,7 +80,7 @@ __device__ __forceinline__ int glob_xcd_block(int i, int total) {
   return x * per + (x < rem ? x : rem) + j;
 }
 
-template <typename T, int HD>
+template <typename T, int HD, bool PRE>
 __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const T* __restrict__ q,
                                                                          const T* __restrict__ kt,
                                                                          const T* __restrict__ v,
@@ -89,10 +92,12 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
   constexpr int kKS = S::kKS, kMBO = S::kMBO, kTile = S::kTile, kVStride = S::kVStride, kVOff = S::kVOff;
   constexpr int kUnitsK = HD / 8;  // DMA units of the kT part of a tile
   typedef typename Vec<T>::x8 X8;
-  constexpr bool kPre = __is_same(T, f16);  // pre-scaled q, bias through the MFMA
-  constexpr bool kSplitP = !kPre;           // bf16: P as hi + lo for the P.V product
+  constexpr bool kF16 = __is_same(T, f16);
+  constexpr bool kPre = PRE;                // pre-scaled q, bias through the MFMA (f16 only)
+  static_assert(!PRE || kF16, "pre-scaled q is an f16 path");
+  constexpr bool kSplitP = !kF16;           // bf16: P as hi + lo for the P.V product
   constexpr int W = 64;
-  constexpr unsigned short kOne = kPre ? 0x3C00 : 0x3F80;
+  constexpr unsigned short kOne = kF16 ? 0x3C00 : 0x3F80;
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   T* kring = reinterpret_cast<T*>(smem);
@@ -359,7 +364,7 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
       }
       b[w4] = pack8(pv, (X8*)nullptr);
       if constexpr (!S::kOnesRows) {
-        if constexpr (kPre) {
+        if constexpr (kF16) {
           typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 #pragma unroll
           for (int e = 0; e < 8; e += 2)
@@ -440,10 +445,10 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
   }
 }
 
-template <typename T, int HD>
+template <typename T, int HD, bool PRE>
 static hipError_t launch_glob(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                               int h, float scale, hipStream_t stream) {
-  auto kern = attn_relpos_glob_kernel<T, HD>;
+  auto kern = attn_relpos_glob_kernel<T, HD, PRE>;
   constexpr size_t lds = glob::Shape<HD>::kLdsBytes;
   static std::atomic<unsigned long long> lds_done{0};
   if (const hipError_t e = lds_opt_in(lds_done, (const void*)kern, (int)lds); e != hipSuccess) return e;
@@ -460,12 +465,16 @@ bool attn_relpos_global(int dtype, const void* q, const void* kt, const void* v,
                         int hd, int h, int w, float scale, hipStream_t stream, hipError_t* err) {
   const float sc = scale * kLog2e;
   if ((hd != 80 && hd != 64) || w != 64 || h < 1 || h > 64 || !(sc >= 0.015625f && sc <= 4.f)) return false;
+  // f16 pre-scales q up to the model's own scale hd^-1/2 (the rounding error grows with the scale)
+  const bool pre = dtype == kF16 && scale * sqrtf((float)hd) <= 1.0001f;
   if (hd == 80)
-    *err = dtype == kF16 ? launch_glob<f16, 80>(q, kt, v, table, out, bh, h, scale, stream)
-                         : launch_glob<bf16, 80>(q, kt, v, table, out, bh, h, scale, stream);
+    *err = dtype != kF16 ? launch_glob<bf16, 80, false>(q, kt, v, table, out, bh, h, scale, stream)
+           : pre         ? launch_glob<f16, 80, true>(q, kt, v, table, out, bh, h, scale, stream)
+                         : launch_glob<f16, 80, false>(q, kt, v, table, out, bh, h, scale, stream);
   else
-    *err = dtype == kF16 ? launch_glob<f16, 64>(q, kt, v, table, out, bh, h, scale, stream)
-                         : launch_glob<bf16, 64>(q, kt, v, table, out, bh, h, scale, stream);
+    *err = dtype != kF16 ? launch_glob<bf16, 64, false>(q, kt, v, table, out, bh, h, scale, stream)
+           : pre         ? launch_glob<f16, 64, true>(q, kt, v, table, out, bh, h, scale, stream)
+                         : launch_glob<f16, 64, false>(q, kt, v, table, out, bh, h, scale, stream);
   return true;
 }
 

@@ -85,3 +85,29 @@ def test_single_row_and_column_grids(hip, h, w, hd, dtype):
     torch.cuda.synchronize()
     want = oracle.attention_relpos(q, kt, v, table, h, w, hd ** -0.5)
     check(got.float().cpu().numpy(), want, dtype, f"line grid {h}x{w} hd={hd} {dtype}")
+
+
+# scales other than hd^-0.5: a sharp 1.0, 0.2 (the f16 global kernel pre-scales q only up to hd^-0.5),
+# a flat 0.03, 0 (uniform weights over the bias) and a negative one (the dedicated window and global
+# kernels take scale > 0; the others go to the general kernel); the wide-grid kernel at 65 x 64
+SCALES = [1.0, 0.2, 0.03, 0.0, -0.1]
+SCALE_GRIDS = [(14, 14, 80), (64, 64, 80), (14, 14, 64), (64, 64, 64), (7, 11, 64), (65, 64, 64)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("h,w,hd", SCALE_GRIDS)
+@pytest.mark.parametrize("scale", SCALES)
+def test_attention_relpos_other_scales(hip, h, w, hd, scale, dtype):
+    if dtype == "f32" and max(h, w) > 64:
+        pytest.skip("f32 rel-pos attention stops at 64 x 64 (larger f32 grids take the reference's sequence)")
+    n = h * w
+    print(f"scale {scale} {dtype} h={h} w={w} hd={hd}", flush=True)
+    r = np.random.default_rng(7500 + n + hd)
+    bh = 2
+    q, kt, v = draw(r, (bh, n, hd), dtype), draw(r, (bh, hd, n), dtype), draw(r, (bh, n, hd), dtype)
+    table = draw(r, (2 * h - 1 + 2 * w - 1, hd), dtype, 0.02)
+    got = hip.attention_relpos(to_dev(q, dtype), to_dev(kt, dtype), to_dev(v, dtype), to_dev(table, dtype), h, w,
+                               scale)
+    torch.cuda.synchronize()
+    want = oracle.attention_relpos(q, kt, v, table, h, w, scale)
+    check(got.float().cpu().numpy(), want, dtype, f"scale {scale} {h}x{w} hd={hd} {dtype}")
