@@ -12,15 +12,11 @@
 //
 // On gfx950 the MFMA and the VALU work of a SIMD barely overlap (measured: the time of a loop is close
 // to the sum of its MFMA and VALU times), and exp2 issues at a quarter of the FMA rate, so the kernel
-// keeps the per-score VALU work to exp2, the tile max and the f32 -> f16 packing:
-//   * f16 at scales up to hd^-1/2 (the model's own): q is pre-scaled by scale*log2(e) and rounded to
-//     f16 once; the MFMA starts from Rw*log2(e) and takes the per-query term Rh - m_run as one extra
-//     k-step (a ones column of K against its f16 hi/lo split), so the accumulator is the exp2 argument
-//     itself. The rounding moves a logit by about 2^-12 of |scale * q . k|: at hd^-1/2 that is the
-//     size of the f16 rounding of the reference's own bmm(q, kT) scores, but it grows with the scale
-//     (scale 1 on N(0, 1) inputs: 8.5e-3 beyond the output's rounding). Larger scales, and bf16 (whose
-//     8-bit mantissa would not absorb the pre-scaling), keep q exact and apply scale and Rh - m_run
-//     with one fma per score (2.5% more time on the ViT-H global layer in f16).
+// keeps the per-score VALU work to exp2 with its fma, the tile max and the f32 -> f16 packing:
+//   * q stays exact: the MFMA starts from Rw*log2(e)/(scale*log2(e)) and one fma per score applies the
+//     scale and Rh - m_run in f32. (Pre-scaling q in f16 would save that fma, 2.5% of the ViT-H global
+//     layer, but its rounding moves a logit by about 2^-12 of |scale * q . k|: q and k of standard
+//     deviation 3, or scale 1 on unit inputs, came out 8e-3 beyond the output's rounding.)
 //   * hd 80: the softmax denominator comes out of the P.V product: the V^T rows 80..95 of the third
 //     32-row block read a ones vector, so O^T rows 80..95 are the running sums of P (as rounded for the
 //     MFMA). hd 64 has no spare rows (two full blocks), so a lane sums its P values on the VALU (v_dot2
@@ -80,7 +76,7 @@ __device__ __forceinline__ int glob_xcd_block(int i, int total) {
   return x * per + (x < rem ? x : rem) + j;
 }
 
-template <typename T, int HD, bool PRE>
+template <typename T, int HD>
 __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const T* __restrict__ q,
                                                                          const T* __restrict__ kt,
                                                                          const T* __restrict__ v,
@@ -93,8 +89,6 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
   constexpr int kUnitsK = HD / 8;  // DMA units of the kT part of a tile
   typedef typename Vec<T>::x8 X8;
   constexpr bool kF16 = __is_same(T, f16);
-  constexpr bool kPre = PRE;                // pre-scaled q, bias through the MFMA (f16 only)
-  static_assert(!PRE || kF16, "pre-scaled q is an f16 path");
   constexpr bool kSplitP = !kF16;           // bf16: P as hi + lo for the P.V product
   constexpr int W = 64;
   constexpr unsigned short kOne = kF16 ? 0x3C00 : 0x3F80;
@@ -171,10 +165,10 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
   scatter(gw, 2 * W - 1, qj, W);
   wave_sync();
   // a lane's key columns in 32-key block mb: 32*mb + 8*(e>>2) + 4*hh + (e&3); the accumulator starts at
-  // Rw*log2(e) (pre-scaled q) or Rw*log2(e) / sc
+  // Rw*log2(e) / sc
   f32x16 cinit[2];
   {
-    const float f = kPre ? 1.f : 1.f / sc;
+    const float f = 1.f / sc;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -182,12 +176,6 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
   }
   wave_sync();
   scatter(gh, 2 * H - 1, qi, H);
-  if (kPre) {
-#pragma unroll
-    for (int s = 0; s < kKS; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[s][e] = (T)((float)qf[s][e] * sc);
-  }
   __syncthreads();  // every wave is done with the table: the kT ring is free
 
   // ---- the DMA ring: tile t (grid row t) into buffer t % 4; past the last tile, reload the last.
@@ -270,14 +258,6 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
         vaddr2[w4][r] = opaque(lds0 + 2 * (kVOff + key * HD + at(8 + c0)));
       }
     }
-  // the extra k-step of the f16 path: K columns 0 and 1 are ones, Q columns 0 and 1 the hi / lo halves of
-  // Rh - m_run (lanes hh == 0 hold k = 0..7)
-  X8 aone{};
-  if (hh == 0) {
-    aone[0] = (T)1.f;
-    aone[1] = (T)1.f;
-  }
-
   float m_run = 0.f;
   float lsum = 0.f;  // hd 64: this lane's share of the softmax denominator
   f32x16 o[kMBO];
@@ -304,20 +284,6 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
   };
-  // f16: + (Rh - m_run) of tile t through the extra k-step, once m_run is known
-  auto qk_b = [&](int t, f32x16* s) {
-    if (kPre) {
-      const bool live = t < ntiles;
-      const float c = rhs[(live ? t : 0) * 32 + n] - m_run;
-      const T hi = live ? (T)c : (T)(-INFINITY);
-      const T lo = live ? (T)(c - (float)(T)c) : (T)0.f;
-      X8 bext{};
-      bext[0] = hh == 0 ? hi : (T)0.f;
-      bext[1] = hh == 0 ? lo : (T)0.f;
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) s[mb] = mma32(aone, bext, s[mb]);
-    }
-  };
   // Softmax and P.V of tile t (scores in s_cur, K/V in buffer buf = t % 4) with the S^T of tile t+1
   // into s_nxt.
   auto step = [&](int t, int buf, f32x16* s_cur, f32x16* s_nxt) {
@@ -327,14 +293,14 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
     dma_part(t + 3, (buf + 3) & 3, 0);
     qk_k((buf + 1) & 3, s_nxt);
     dma_part(t + 3, (buf + 3) & 3, 1);
-    // exp2 argument: x = s (f16) or s*sc + c (bf16), relative to m_run
-    const float c = kPre ? 0.f : (t < ntiles ? rhs[t * 32 + n] - m_run : -INFINITY);
+    // exp2 argument: s*sc + c, relative to m_run
+    const float c = t < ntiles ? rhs[t * 32 + n] - m_run : -INFINITY;
     float mm = s_cur[0][0];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mm = max_nc(mm, s_cur[mb][e]);
-    const float mt = max_with_partner32(kPre ? mm : fmaf(mm, sc, c));
+    const float mt = max_with_partner32(fmaf(mm, sc, c));
     float cc = c;
     if (wave_any(t == 0 || mt > kSlack)) {
       // the first tile sets m_run; later ones raise it when a score exceeds it by more than the slack
@@ -344,14 +310,8 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
       for (int ob = 0; ob < kMBO; ++ob) o[ob] *= alpha;
       if constexpr (!S::kOnesRows) lsum *= alpha;
       m_run += delta;
-      if (kPre) {
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) s_cur[mb] -= delta;
-      } else {
-        cc -= delta;
-      }
+      cc -= delta;
     }
-    qk_b(t + 1, s_nxt);
     dma_part(t + 3, (buf + 3) & 3, 2);
     X8 b[4], blo[4];
 #pragma unroll
@@ -360,7 +320,7 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float x = s_cur[w4 >> 1][8 * (w4 & 1) + e];
-        pv[e] = exp2_fast(kPre ? x : fmaf(x, sc, cc));
+        pv[e] = exp2_fast(fmaf(x, sc, cc));
       }
       b[w4] = pack8(pv, (X8*)nullptr);
       if constexpr (!S::kOnesRows) {
@@ -410,7 +370,6 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
   wait_tiles(std::integral_constant<int, 2>());  // tile 0 has landed (tiles 1, 2 may be in flight)
   __syncthreads();
   qk_k(0, sa);
-  qk_b(0, sa);
   // unrolled by the ring depth, so that every buffer offset is a constant; tiles past the last (up to
   // the next multiple of 4) are masked: their bias is -inf, so they add nothing
   for (int t = 0; t < ntiles; t += 4) {
@@ -445,10 +404,10 @@ __global__ __launch_bounds__(glob::kThreads) void attn_relpos_glob_kernel(const 
   }
 }
 
-template <typename T, int HD, bool PRE>
+template <typename T, int HD>
 static hipError_t launch_glob(const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                               int h, float scale, hipStream_t stream) {
-  auto kern = attn_relpos_glob_kernel<T, HD, PRE>;
+  auto kern = attn_relpos_glob_kernel<T, HD>;
   constexpr size_t lds = glob::Shape<HD>::kLdsBytes;
   static std::atomic<unsigned long long> lds_done{0};
   if (const hipError_t e = lds_opt_in(lds_done, (const void*)kern, (int)lds); e != hipSuccess) return e;
@@ -465,16 +424,12 @@ bool attn_relpos_global(int dtype, const void* q, const void* kt, const void* v,
                         int hd, int h, int w, float scale, hipStream_t stream, hipError_t* err) {
   const float sc = scale * kLog2e;
   if ((hd != 80 && hd != 64) || w != 64 || h < 1 || h > 64 || !(sc >= 0.015625f && sc <= 4.f)) return false;
-  // f16 pre-scales q up to the model's own scale hd^-1/2 (the rounding error grows with the scale)
-  const bool pre = dtype == kF16 && scale * sqrtf((float)hd) <= 1.0001f;
   if (hd == 80)
-    *err = dtype != kF16 ? launch_glob<bf16, 80, false>(q, kt, v, table, out, bh, h, scale, stream)
-           : pre         ? launch_glob<f16, 80, true>(q, kt, v, table, out, bh, h, scale, stream)
-                         : launch_glob<f16, 80, false>(q, kt, v, table, out, bh, h, scale, stream);
+    *err = dtype == kF16 ? launch_glob<f16, 80>(q, kt, v, table, out, bh, h, scale, stream)
+                         : launch_glob<bf16, 80>(q, kt, v, table, out, bh, h, scale, stream);
   else
-    *err = dtype != kF16 ? launch_glob<bf16, 64, false>(q, kt, v, table, out, bh, h, scale, stream)
-           : pre         ? launch_glob<f16, 64, true>(q, kt, v, table, out, bh, h, scale, stream)
-                         : launch_glob<f16, 64, false>(q, kt, v, table, out, bh, h, scale, stream);
+    *err = dtype == kF16 ? launch_glob<f16, 64>(q, kt, v, table, out, bh, h, scale, stream)
+                         : launch_glob<bf16, 64>(q, kt, v, table, out, bh, h, scale, stream);
   return true;
 }
 

@@ -111,3 +111,55 @@ def test_attention_relpos_other_scales(hip, h, w, hd, scale, dtype):
     torch.cuda.synchronize()
     want = oracle.attention_relpos(q, kt, v, table, h, w, scale)
     check(got.float().cpu().numpy(), want, dtype, f"scale {scale} {h}x{w} hd={hd} {dtype}")
+
+
+# larger activations at the model's own scale hd^-0.5: q and k of standard deviation 2 and 3 (logits 4
+# and 9 times those of unit inputs), v of 1. In f32 the oracle's own sequential f32 arithmetic (the
+# reference's, kernels.rs:197-214) is itself up to 1.3e-5 from the exact value on these draws (64 x 64,
+# standard deviation 2), so f32 is held to the 1e-5 bar against a float64 evaluation of the formula and
+# its distance to the oracle is printed beside the oracle's own.
+MAGNITUDES = [2.0, 3.0]
+
+
+def attention_relpos_f64(q, kt, v, table, h, w, scale):
+    """The fused rel-pos attention in float64 (textbook form, for the f32 bar)."""
+    n = h * w
+    th, tw = table[: 2 * h - 1].astype(np.float64), table[2 * h - 1:].astype(np.float64)
+    ri, rj = np.arange(n) // w, np.arange(n) % w
+    rows = np.arange(n)[:, None]
+    out = np.empty(q.shape, np.float64)
+    for b in range(q.shape[0]):
+        qq = q[b].astype(np.float64)
+        s = qq @ kt[b].astype(np.float64) * scale
+        s += (qq @ th.T)[rows, ri[:, None] - ri[None, :] + h - 1] + (qq @ tw.T)[rows, rj[:, None] - rj[None, :] + w - 1]
+        p = np.exp(s - s.max(1, keepdims=True))
+        out[b] = (p / p.sum(1, keepdims=True)) @ v[b].astype(np.float64)
+    return out
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("h,w,hd", [(14, 14, 80), (64, 64, 80), (64, 64, 64), (7, 11, 64)])
+@pytest.mark.parametrize("std", MAGNITUDES)
+def test_attention_relpos_larger_activations(hip, h, w, hd, std, dtype):
+    n = h * w
+    print(f"std {std} {dtype} h={h} w={w} hd={hd}", flush=True)
+    r = np.random.default_rng(7600 + n + hd + int(10 * std))
+    bh = 2
+    q, kt = draw(r, (bh, n, hd), dtype, std), draw(r, (bh, hd, n), dtype, std)
+    v = draw(r, (bh, n, hd), dtype)
+    table = draw(r, (2 * h - 1 + 2 * w - 1, hd), dtype, 0.02)
+    got = hip.attention_relpos(to_dev(q, dtype), to_dev(kt, dtype), to_dev(v, dtype), to_dev(table, dtype), h, w,
+                               hd ** -0.5)
+    torch.cuda.synchronize()
+    got = got.float().cpu().numpy()
+    want = oracle.attention_relpos(q, kt, v, table, h, w, hd ** -0.5)
+    if dtype == "f32":
+        exact = attention_relpos_f64(q, kt, v, table, h, w, hd ** -0.5)
+        e64 = np.abs(got - exact).max() / np.abs(exact).max()
+        eor = np.abs(got - want).max() / np.abs(want).max()
+        own = np.abs(want - exact).max() / np.abs(exact).max()
+        print(f"parity std {std} {h}x{w} hd={hd} f32: vs float64 {e64:.3g}, vs oracle {eor:.3g} (oracle vs "
+              f"float64 {own:.3g})", flush=True)
+        assert e64 <= 1e-5
+    else:
+        check(got, want, dtype, f"std {std} {h}x{w} hd={hd} {dtype}")
