@@ -21,7 +21,7 @@
 //
 // Few query blocks (SAM 2 memory attention: one head, 4096 queries, 4096 or 28736 keys) would leave
 // most of the 256 CUs idle, so the keys are split across workgroups; each split writes a partial O
-// (f16: normalised by its own sum, in f16, half the bytes of f32; bf16: unnormalised, in f32) with its
+// (unnormalised, in f32) with its
 // running max and sum, and flash_combine_kernel merges the splits by log-sum-exp. Workgroups are
 // numbered XCD-major with all query blocks of one (head, split) adjacent, so the K/V range of a split
 // is fetched into one XCD's L2 and shared there.
@@ -295,20 +295,28 @@ __global__ __launch_bounds__(NW * 64, NW == 4 && DP <= 64 && __is_same(T, f16) ?
       const float c = MASK && m_run == -INFINITY ? 0.f : -m_run;
       constexpr float one = 1.f;
       const float scs = MASK ? one : sc;  // the masked scores are scaled already
+      // P, and its sum as the P.V product sees it: f16 sums the rounded P (v_dot2 with ones), so that
+      // numerator and denominator weigh each key alike (a dominant key's rounding cancels); bf16 (P as
+      // hi + lo) sums the f32 P
       float lsum = 0.f;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         float pv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          pv[j] = exp2_fast(fmaf(s_cur[u >> 1][8 * (u & 1) + j], scs, c));
-          lsum += pv[j];
-        }
+        for (int j = 0; j < 8; ++j) pv[j] = exp2_fast(fmaf(s_cur[u >> 1][8 * (u & 1) + j], scs, c));
         b[u] = pack8(pv, (X8*)nullptr);
-        if (kSplitP) {
+        if constexpr (kSplitP) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) pv[j] -= to_f32(b[u][j]);
+          for (int j = 0; j < 8; ++j) {
+            lsum += pv[j];
+            pv[j] -= to_f32(b[u][j]);
+          }
           blo[u] = pack8(pv, (X8*)nullptr);
+        } else {
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+          for (int j = 0; j < 8; j += 2)
+            lsum = __builtin_amdgcn_fdot2(h2{b[u][j], b[u][j + 1]}, h2{(f16)1.f, (f16)1.f}, lsum, false);
         }
       }
       l_run += lsum;
@@ -367,35 +375,19 @@ __global__ __launch_bounds__(NW * 64, NW == 4 && DP <= 64 && __is_same(T, f16) ?
         }
       }
   } else {
-    // partial O [split][bh][q][DP] and (max, sum) [split][bh][q][2]: f16 stores O / sum (a convex
-    // combination of f16 values of v, so it stays in range), bf16 the unnormalised O in f32
+    // partial O [split][bh][q][DP] (unnormalised, f32) and (max, sum) [split][bh][q][2]
     const long row = ((long)split * p.b * p.h + bhi) * p.lq + qidx;
-    if constexpr (__is_same(T, f16)) {
-      const float inv = MASK && l == 0.f ? 0.f : 1.f / l;  // a split whose keys are all masked: 0, weight 0
-      f16* prow = reinterpret_cast<f16*>(p.opart) + row * DP;
+    float* prow = p.opart + row * DP;
 #pragma unroll
-      for (int ob = 0; ob < MBO; ++ob)
+    for (int ob = 0; ob < MBO; ++ob)
 #pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const int d0 = 32 * ob + 8 * a + 4 * hh;
-          Vec<f16>::x4 w4;
+      for (int a = 0; a < 4; ++a) {
+        const int d0 = 32 * ob + 8 * a + 4 * hh;
+        f32x4 w4;
 #pragma unroll
-          for (int bb = 0; bb < 4; ++bb) w4[bb] = (f16)(o[ob][4 * a + bb] * inv);
-          *reinterpret_cast<Vec<f16>::x4*>(prow + d0) = w4;
-        }
-    } else {
-      float* prow = p.opart + row * DP;
-#pragma unroll
-      for (int ob = 0; ob < MBO; ++ob)
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const int d0 = 32 * ob + 8 * a + 4 * hh;
-          f32x4 w4;
-#pragma unroll
-          for (int bb = 0; bb < 4; ++bb) w4[bb] = o[ob][4 * a + bb];
-          *reinterpret_cast<f32x4*>(prow + d0) = w4;
-        }
-    }
+        for (int bb = 0; bb < 4; ++bb) w4[bb] = o[ob][4 * a + bb];
+        *reinterpret_cast<f32x4*>(prow + d0) = w4;
+      }
     if (hh == 0) {
       float2 ml;
       ml.x = m_run;
@@ -406,9 +398,8 @@ __global__ __launch_bounds__(NW * 64, NW == 4 && DP <= 64 && __is_same(T, f16) ?
 }
 
 // out[b, q, h, :] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, M = max_s m_s, with O_s the
-// unnormalised partial (bf16: f32 partials) or l_s times the stored O_s / l_s (f16: f16 partials).
-// A row takes DP / 8 lanes of 8 consecutive columns each (one 16-byte read per split of an f16
-// partial, two of an f32 one), so a workgroup merges 256 / (DP / 8) rows.
+// unnormalised f32 partial. A row takes DP / 8 lanes of 8 consecutive columns each (two 16-byte reads
+// per split), so a workgroup merges 256 / (DP / 8) rows.
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p) {
   constexpr int LPR = DP / 8;     // lanes per row
@@ -431,18 +422,12 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p) {
       const long r = ((long)(s0 + j) * plane + row);
       if (s0 + j < p.nsplit) {
         ml[j] = *reinterpret_cast<const float2*>(p.ml + r * 2);
-        if constexpr (__is_same(T, f16)) {
-          const f16x8 o8 = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(p.opart) + r * DP + c);
+        const f32x4* src = reinterpret_cast<const f32x4*>(p.opart + r * DP + c);
+        const f32x4 a = src[0], b = src[1];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) o[j][k] = (float)o8[k];
-        } else {
-          const f32x4* src = reinterpret_cast<const f32x4*>(p.opart + r * DP + c);
-          const f32x4 a = src[0], b = src[1];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            o[j][k] = a[k];
-            o[j][4 + k] = b[k];
-          }
+        for (int k = 0; k < 4; ++k) {
+          o[j][k] = a[k];
+          o[j][4 + k] = b[k];
         }
       } else {
         ml[j] = make_float2(-INFINITY, 0.f);
@@ -467,9 +452,8 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(FlashParams p) {
       const float w = ml[j].x == -INFINITY ? 0.f : exp2_fast(ml[j].x - mx);
       const float wl = w * ml[j].y;
       den += wl;
-      const float f = __is_same(T, f16) ? wl : w;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) acc[k] += f * o[j][k];
+      for (int k = 0; k < 8; ++k) acc[k] += w * o[j][k];
     }
   }
   if (c >= p.d) return;

@@ -300,24 +300,11 @@ __global__ __launch_bounds__(f256::kThreads) void flash256_kernel(FlashParams p)
       *reinterpret_cast<typename Vec<T>::x4*>(orow + 16 * db + 4 * g) = w4;
     }
   } else {
-    // partial O [split][bh][q][256] and (max, sum) [split][bh][q][2]: f16 stores O / sum (a convex
-    // combination of f16 values of v, so it stays in range), bf16 the unnormalised O in f32
+    // partial O [split][bh][q][256] (unnormalised, f32) and (max, sum) [split][bh][q][2]
     const long row = ((long)split * p.b * p.h + bhi) * p.lq + qidx;
-    if constexpr (__is_same(T, f16)) {
-      const float inv = 1.f / l;
-      f16* prow = reinterpret_cast<f16*>(p.opart) + row * 256;
+    float* prow = p.opart + row * 256;
 #pragma unroll
-      for (int db = 0; db < 16; ++db) {
-        Vec<f16>::x4 w4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w4[i] = (f16)(o[db][i] * inv);
-        *reinterpret_cast<Vec<f16>::x4*>(prow + 16 * db + 4 * g) = w4;
-      }
-    } else {
-      float* prow = p.opart + row * 256;
-#pragma unroll
-      for (int db = 0; db < 16; ++db) *reinterpret_cast<f32x4*>(prow + 16 * db + 4 * g) = o[db];
-    }
+    for (int db = 0; db < 16; ++db) *reinterpret_cast<f32x4*>(prow + 16 * db + 4 * g) = o[db];
     if (g == 0) {
       float2 ml;
       ml.x = m_run;
