@@ -177,3 +177,21 @@ def test_flash_attn_larger_activations(hip, b, lq, lk, h, d, dtype):
     got = hip.flash_attn(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype))
     torch.cuda.synchronize()
     check(got.float().cpu().numpy(), oracle.mha_blhd(q, k, v), dtype, f"flash std 3 b{b} lq{lq} lk{lk} h{h} d{d} {dtype}")
+
+
+# relpos_softmax over large scores (standard deviation 10: rows dominated by a few keys) on the window
+# grid (16 lanes per row), the global grid (vector kernel) and an odd-length row (scalar kernel)
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("h,w,hd", [(14, 14, 80), (64, 64, 80), (5, 9, 64)])
+def test_relpos_softmax_large_scores(hip, h, w, hd, dtype):
+    n = h * w
+    print(f"relpos_softmax std 10 {dtype} h={h} w={w} hd={hd}", flush=True)
+    r = np.random.default_rng(7800 + n + hd)
+    bh = 2
+    s = draw(r, (bh, n, n), dtype, 10.0)
+    q = draw(r, (bh, n, hd), dtype)
+    t = draw(r, (2 * h - 1 + 2 * w - 1, hd), dtype)
+    got = hip.relpos_softmax(to_dev(s, dtype), to_dev(q, dtype), to_dev(t, dtype), h, w, 0.125)
+    torch.cuda.synchronize()
+    want = oracle.relpos_softmax(s, q, t, h, w, 0.125)
+    check(got.float().cpu().numpy(), want, dtype, f"relpos_softmax std 10 {h}x{w} hd={hd} {dtype}")
