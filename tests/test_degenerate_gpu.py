@@ -138,9 +138,11 @@ def attention_relpos_f64(q, kt, v, table, h, w, scale):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
-@pytest.mark.parametrize("h,w,hd", [(14, 14, 80), (64, 64, 80), (64, 64, 64), (7, 11, 64)])
+@pytest.mark.parametrize("h,w,hd", [(14, 14, 80), (64, 64, 80), (64, 64, 64), (7, 11, 64), (65, 64, 64), (96, 96, 80)])
 @pytest.mark.parametrize("std", MAGNITUDES)
 def test_attention_relpos_larger_activations(hip, h, w, hd, std, dtype):
+    if dtype == "f32" and max(h, w) > 64:
+        pytest.skip("f32 rel-pos attention stops at 64 x 64 (larger f32 grids take the reference's sequence)")
     n = h * w
     print(f"std {std} {dtype} h={h} w={w} hd={hd}", flush=True)
     r = np.random.default_rng(7600 + n + hd + int(10 * std))
