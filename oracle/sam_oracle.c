@@ -178,6 +178,15 @@ void oracle_qkv_rope(const float* y, const float* bias, const float* cos_t, cons
   }
 }
 
+/* x.floor() as i64 in Rust (kernels.rs:799-800): NaN gives 0 and out-of-range values saturate. The clamp
+   to +-2^62 leaves every comparison with a level's size as it is and keeps x0 + 1 from overflowing. */
+static long floor_as_index(float xf) {
+  if (xf != xf) return 0;
+  if (xf >= 4.6e18f) return 1L << 62;
+  if (xf <= -4.6e18f) return -(1L << 62);
+  return (long)xf;
+}
+
 void oracle_deform_attn(const float* value, const float* loc, const float* attn, float* out, int b, int s, int q, int h,
                         int d, int l, int p, const int* shapes, int nthreads) {
   long starts[64];
@@ -202,7 +211,7 @@ void oracle_deform_attn(const float* value, const float* loc, const float* attn,
           const float x = loc[base * 2] * (float)wl - 0.5f;
           const float y = loc[base * 2 + 1] * (float)hl - 0.5f;
           const float xf = floorf(x), yf = floorf(y);
-          const long x0 = (long)xf, y0 = (long)yf;
+          const long x0 = floor_as_index(xf), y0 = floor_as_index(yf);
           const float fx = x - xf, fy = y - yf;
           for (int c = 0; c < 4; ++c) {
             const long xx = x0 + (c & 1), yy = y0 + (c >> 1);

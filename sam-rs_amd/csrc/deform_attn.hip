@@ -39,6 +39,13 @@ struct Levels {
   int start[kDeformMaxLevels];
 };
 
+// floor(x) as an index, as the reference's `x.floor() as i64` takes it (kernels.rs:799-800): NaN gives 0,
+// large values saturate; the clamp to +-2^30 keeps the conversion defined and the corner x0 + 1 from
+// overflowing, and any index that far out lies outside every level
+__device__ __forceinline__ int floor_index(float xf) {
+  return xf != xf ? 0 : (int)fminf(fmaxf(xf, -1073741824.f), 1073741824.f);
+}
+
 template <typename T, int VEC> struct VecLoad;
 template <> struct VecLoad<float, 4> { typedef f32x4 type; };
 template <> struct VecLoad<f16, 8> { typedef f16x8 type; };
@@ -144,7 +151,7 @@ __global__ __launch_bounds__(kDeformThreads) void deform_attn_kernel(const T* __
       const float x = lx * (float)Wl - 0.5f;
       const float y = ly * (float)Hl - 0.5f;
       const float xf = floorf(x), yf = floorf(y);
-      const int x0 = (int)xf, y0 = (int)yf;
+      const int x0 = floor_index(xf), y0 = floor_index(yf);
       const float fx = x - xf, fy = y - yf;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -303,7 +310,7 @@ __global__ __launch_bounds__(kDeformThreads) void deform_attn_gather_kernel(cons
       const float x = lx * (float)Wl - 0.5f;
       const float y = ly * (float)Hl - 0.5f;
       const float xf = floorf(x), yf = floorf(y);
-      const int x0 = (int)xf, y0 = (int)yf;
+      const int x0 = floor_index(xf), y0 = floor_index(yf);
       const float fx = x - xf, fy = y - yf;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {

@@ -119,3 +119,28 @@ def test_deform_errors(hip):
     a = torch.zeros(1, 3, 2, 2, 2, device="cuda")
     with pytest.raises(hip.SamHipError, match="pixels"):
         hip.deform_attn(v, loc, a, [(2, 3), (2, 3)])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("d", [32, 6])
+def test_degenerate_sampling_locations(hip, d, dtype):
+    """Sampling locations the reference takes without complaint: exactly on the edges (0 and 1), far
+    outside the levels (+-3, +-1e10) and NaN. The reference's `x.floor() as i64` (kernels.rs:799-800)
+    saturates and maps NaN to 0, so a far-out point adds nothing and a NaN point's corner (0, 0) is
+    read with a NaN weight: the output columns of that query and head are NaN. The oracle follows
+    that cast; the kernel must give the same NaN pattern and the usual bars elsewhere. Both the
+    16-byte-lane kernel (d 32) and the scalar-lane kernel (d 6) run."""
+    shapes = [(20, 30), (10, 15), (5, 8), (3, 4)]
+    value, loc, attn = inputs(shapes, 1, 300, 8, d, 4, 8800 + d, 0.5, dtype)
+    flat = loc.reshape(-1, 2)
+    r = np.random.default_rng(8801)
+    idx = r.permutation(flat.shape[0])
+    for k, val in enumerate([0.0, 1.0, 3.0, -3.0, 1e10, -1e10, np.nan]):
+        sel = idx[k * 40:(k + 1) * 40]
+        flat[sel, k % 2] = val
+    loc = oracle.round_to(loc, dtype)  # f16 takes +-1e10 as +-inf: still outside every level
+    print(f"deform degenerate locations d={d} {dtype}", flush=True)
+    got = run(hip, [value, loc, attn], shapes, dtype)
+    want = oracle.deform_attn(value, loc, attn, shapes)
+    assert np.isnan(want).any() and (np.isnan(got) == np.isnan(want)).all(), "NaN pattern differs"
+    check(np.nan_to_num(got), np.nan_to_num(want), dtype, f"deform degenerate locations d={d} {dtype}")

@@ -184,6 +184,29 @@ def test_deform_matches_scalar_spec_and_grid_sample(oracle_lib, shapes, b, q, h,
     assert np.abs(got - naive).max() < 1e-5
 
 
+def test_deform_degenerate_locations_follow_the_reference_cast(oracle_lib):
+    """The reference takes a corner index as `x.floor() as i64` (kernels.rs:799-800), Rust's saturating
+    cast: NaN gives 0, so a NaN coordinate reads corner 0 of that axis with a NaN weight and the output
+    is NaN; +-1e10 and +-inf saturate far outside the level and add nothing; the edges 0 and 1 give the
+    half-weighted border pixel (x = -0.5 and W - 0.5). A C cast of NaN is undefined (x86 gives INT_MIN,
+    which would skip the corner), so the oracle spells the Rust cast out."""
+    shapes = [(4, 5)]
+    value = np.arange(20, dtype=np.float32).reshape(1, 20, 1, 1) + 1.0  # pixel k holds k + 1
+    pts = [(0.5, np.nan), (np.nan, 0.5), (1e10, 0.5), (-np.inf, 0.5), (0.0, 0.5), (1.0, 0.5), (0.5, 0.5)]
+    loc = np.array(pts, np.float32).reshape(1, len(pts), 1, 1, 1, 2)
+    attn = np.ones((1, len(pts), 1, 1, 1), np.float32)
+    got = oracle_lib.deform_attn(value, loc, attn, shapes)[0, :, 0]
+    assert np.isnan(got[0]) and np.isnan(got[1])
+    assert got[2] == 0.0 and got[3] == 0.0
+    # x = 0: x = -0.5, corners at columns -1 (outside) and 0 with weight 0.5 each; y = 0.5 * 4 - 0.5 =
+    # 1.5, rows 1 and 2 with weight 0.5: 0.25 * (pixel 5 + pixel 10) = 0.25 * (6 + 11)
+    assert got[4] == np.float32(0.25 * (6 + 11))
+    # x = 1: x = 4.5, columns 4 and 5 (outside): 0.25 * (pixel 9 + pixel 14) = 0.25 * (10 + 15)
+    assert got[5] == np.float32(0.25 * (10 + 15))
+    # the centre: x = 2, y = 1.5: columns 2 and 3 with weights 1 and 0, rows 1 and 2 with 0.5 each
+    assert got[6] == np.float32(0.5 * (8 + 13))
+
+
 def _prep_inputs(shapes, b, q, h, p, nc, seed):
     r = _rng(seed)
     l = len(shapes)
