@@ -40,7 +40,7 @@ def run(hip, img, nh, nw, size, dtype, mean=None, std=None):
 
 
 LONGEST_SIDE = [(1080, 1920, 1024), (1920, 1080, 1024), (480, 640, 1024), (1365, 2048, 1024), (37, 53, 64),
-                (1000, 9, 128), (3000, 4000, 1024), (2900, 1900, 96)]
+                (1000, 9, 128), (3000, 4000, 1024), (2900, 1900, 96), (1, 1, 64), (2, 1, 1024), (1, 3, 1024)]
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
