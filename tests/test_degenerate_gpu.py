@@ -197,3 +197,22 @@ def test_relpos_softmax_large_scores(hip, h, w, hd, dtype):
     torch.cuda.synchronize()
     want = oracle.relpos_softmax(s, q, t, h, w, 0.125)
     check(got.float().cpu().numpy(), want, dtype, f"relpos_softmax std 10 {h}x{w} hd={hd} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("c", [1280, 768, 1024])
+def test_bias_residual_ln_constant_rows(hip, c, dtype):
+    """Rows whose residual sum is constant have zero variance: the LayerNorm gives (x - mean) = 0 times
+    1/sqrt(eps), so the normed row is ln_b exactly, and x itself is the constant."""
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    g = torch.Generator(device="cuda").manual_seed(7900 + c)
+    rows = 300
+    res = torch.full((rows, c), 0.75, dtype=tdt, device="cuda")
+    y = torch.full((rows, c), -0.25, dtype=tdt, device="cuda")
+    bias = torch.zeros(c, dtype=tdt, device="cuda")
+    ln_w = torch.randn(c, device="cuda", generator=g).to(tdt)
+    ln_b = torch.randn(c, device="cuda", generator=g).to(tdt)
+    x, normed = hip.bias_residual_ln(res, y, bias, ln_w, ln_b)
+    torch.cuda.synchronize()
+    assert (x == 0.5).all()
+    assert torch.equal(normed, ln_b.expand(rows, c))
