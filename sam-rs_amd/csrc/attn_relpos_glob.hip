@@ -418,8 +418,9 @@ static hipError_t launch_glob(const void* q, const void* kt, const void* v, cons
 }
 
 // The 64-column global grid (W == 64, H <= 64, hd 80 or 64); returns false (nothing launched) for shapes
-// it does not take. The f16 path pre-scales q by scale*log2(e), so that factor must keep f16 q normal
-// and finite: 2^-6 <= scale*log2(e) <= 4 (SAM's hd^-0.5 * log2(e) = 0.16).
+// it does not take. The accumulator starts at Rw*log2(e) / (scale*log2(e)), so the factor must be
+// positive; 2^-6 <= scale*log2(e) <= 4 (SAM's hd^-0.5 * log2(e) = 0.16) keeps that start value and the
+// scaled logits of ordinary size. Other scales take the general kernel.
 bool attn_relpos_global(int dtype, const void* q, const void* kt, const void* v, const void* table, void* out, int bh,
                         int hd, int h, int w, float scale, hipStream_t stream, hipError_t* err) {
   const float sc = scale * kLog2e;
