@@ -105,3 +105,30 @@ def test_every_entry_point_is_deterministic(hip):
             torch.cuda.synchronize()
             for a, b in zip(got, ref):
                 assert torch.equal(a, b), f"{name}: repetition {rep + 1} differs"
+
+
+def test_concurrent_streams_match_sequential_calls(hip):
+    """Entry points launched on two streams at once (both at the default priority) give the results of
+    the same calls made one after the other: no kernel keeps state outside its own call's buffers (the
+    no-allocation entry point's shared array is the documented exception and is not used here)."""
+    g = torch.Generator(device="cuda").manual_seed(5)
+    f16 = torch.float16
+    wq, wk, wv = rnd(g, (400, 196, 80), f16), rnd(g, (400, 80, 196), f16), rnd(g, (400, 196, 80), f16)
+    wt = rnd(g, (54, 80), f16, 0.02)
+    gq, gk, gv = rnd(g, (16, 4096, 80), f16), rnd(g, (16, 80, 4096), f16), rnd(g, (16, 4096, 80), f16)
+    gt = rnd(g, (254, 80), f16, 0.02)
+    fq, fk, fv = rnd(g, (1, 1000, 2, 64), f16), rnd(g, (1, 8000, 2, 64), f16), rnd(g, (1, 8000, 2, 64), f16)
+    a = [lambda: hip.attention_relpos(wq, wk, wv, wt, 14, 14, 80 ** -0.5), lambda: hip.flash_attn(fq, fk, fv)]
+    b = [lambda: hip.attention_relpos(gq, gk, gv, gt, 64, 64, 80 ** -0.5), lambda: hip.flash_attn(fq, fk, fv)]
+    want = [[f() for f in a], [f() for f in b]]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for rep in range(3):
+        print(f"concurrent streams, repetition {rep + 1}", flush=True)
+        with torch.cuda.stream(s1):
+            got_a = [f() for f in a]
+        with torch.cuda.stream(s2):
+            got_b = [f() for f in b]
+        torch.cuda.synchronize()
+        for got, ref in zip(got_a + got_b, want[0] + want[1]):
+            assert torch.equal(got, ref)
