@@ -81,7 +81,7 @@ __global__ __launch_bounds__(bias::kThreads) void bias_ops_kernel(const T* res, 
         for (int k = 0; k < n; ++k) o[k] = from_f32<T>(to_f32(rv[k]) + to_f32(yv[k]) + to_f32(bv[k]));
       } else {
 #pragma unroll
-        for (int k = 0; k < n; ++k) o[k] = from_f32<T>(gelu_erf(to_f32(yv[k]) + to_f32(bv[k])));
+        for (int k = 0; k < n; ++k) o[k] = from_f32<T>(f32_result(gelu_erf(to_f32(yv[k]) + to_f32(bv[k]))));
       }
       *reinterpret_cast<V*>(out + e) = o;
     }
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(bias::kThreads) void bias_ops_kernel(const T* res, 
       if constexpr (MODE == 0)
         out[i] = from_f32<T>(to_f32(res[i]) + to_f32(y[i]) + bb);
       else
-        out[i] = from_f32<T>(gelu_erf(to_f32(y[i]) + bb));
+        out[i] = from_f32<T>(f32_result(gelu_erf(to_f32(y[i]) + bb)));
     }
   }
 }

@@ -78,6 +78,15 @@ template <> __device__ __forceinline__ float from_f32<float>(float v) { return v
 template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return (f16)v; }
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
 
+// v as a finished f32 result. Without it the compiler may fold the multiply that produced v into the
+// conversion that follows (v_fma_mixlo_f16), rounding the exact product to f16 once, where the f32
+// multiply and then the conversion round twice, as the reference's f32 arithmetic does: the two differ
+// by one f16 ulp when the f32 product lands on an f16 rounding midpoint.
+__device__ __forceinline__ float f32_result(float v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 // D(32x32, f32) += A(32x16) * B(16x32). Lane l supplies A[l%32][8*(l/32)+j] and B[8*(l/32)+j][l%32],
 // j = 0..7; it receives D[8*(i/4) + 4*(l/32) + i%4][l%32] in element i (layout checked on gfx950).
 __device__ __forceinline__ f32x16 mma32(f16x8 a, f16x8 b, f32x16 c) {

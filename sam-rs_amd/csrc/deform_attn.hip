@@ -89,7 +89,7 @@ __device__ __forceinline__ float round_t(float x) {
   if constexpr (__is_same(T, float))
     return x;
   else
-    return to_f32(from_f32<T>(x));
+    return to_f32(from_f32<T>(f32_result(x)));
 }
 
 template <typename T, int NC>

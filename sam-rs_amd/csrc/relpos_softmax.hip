@@ -511,7 +511,7 @@ __global__ __launch_bounds__(rsm::kWaves * 64) void relpos_softmax_scalar_kernel
     for (int k = lane; k < N; k += 64) {
       const int kh = k / W, kw = k - kh * W;
       const float x = (to_f32(srow[k]) * scale + brow[W + kh]) + brow[kw];
-      orow[k] = from_f32<T>(exp2_fast((x - mw) * kLog2e) * inv);
+      orow[k] = from_f32<T>(f32_result(exp2_fast((x - mw) * kLog2e) * inv));
     }
   }
 }

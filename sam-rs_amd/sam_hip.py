@@ -131,6 +131,13 @@ def _dtype(*ts: torch.Tensor) -> int:
     return _DTYPES[dt]
 
 
+def _aligned16(*ts: torch.Tensor):
+    """The tensors, with any that starts off a 16-byte boundary (a view with a storage offset) replaced by
+    a copy: the kernels move 16-byte vectors, and a fresh allocation is always aligned. The reference's
+    kernels take such views, so the copy keeps the call a drop-in instead of an error."""
+    return tuple(t if t.data_ptr() % 16 == 0 else t.clone() for t in ts)
+
+
 def _contig(*ts: torch.Tensor):
     for t in ts:
         if not t.is_cuda:
@@ -148,6 +155,7 @@ def attention_relpos(q: torch.Tensor, kt: torch.Tensor, v: torch.Tensor, table: 
     q, v: [BH, h*w, hd]; kt: [BH, hd, h*w]; table: rel_pos_h rows followed by rel_pos_w rows,
     [(2h-1)+(2w-1), hd]. Returns [BH, h*w, hd] in the inputs' dtype.
     """
+    q, kt, v, table = _aligned16(q, kt, v, table)
     _contig(q, kt, v, table)
     dt = _dtype(q, kt, v, table)
     bh, n, hd = q.shape
@@ -168,6 +176,7 @@ def deform_attn(value: torch.Tensor, loc: torch.Tensor, attn: torch.Tensor, shap
     the reference does (kernels.rs:825).
     """
     value, loc, attn = value.contiguous(), loc.contiguous(), attn.contiguous()
+    value, loc, attn = _aligned16(value, loc, attn)
     _contig(value, loc, attn)
     dt = _dtype(value, loc, attn)
     b, s, h, d = value.shape
@@ -192,6 +201,7 @@ def deform_core(value: torch.Tensor, offsets: torch.Tensor, logits: torch.Tensor
     and reference points refs [B, Q, L, 2] (encoder: ref + off / (W, H)) or [B, Q, L, 4] (decoder:
     xy + off / P * wh * 0.5), then the bilinear gather of value [B, S, H, D] -> [B, Q, H*D]."""
     value, offsets, logits, refs = (t.contiguous() for t in (value, offsets, logits, refs))
+    value, offsets, logits, refs = _aligned16(value, offsets, logits, refs)
     _contig(value, offsets, logits, refs)
     dt = _dtype(value, offsets, logits, refs)
     b, s, h, d = value.shape
@@ -235,6 +245,7 @@ def bias_residual_ln(res: torch.Tensor, y: torch.Tensor, bias: torch.Tensor, ln_
     in one pass: -> (x = res + y + bias, LayerNorm(x) * ln_w + ln_b), the norm taken over x as rounded
     to the dtype."""
     res, y, bias, ln_w, ln_b = (t.contiguous() for t in (res, y, bias, ln_w, ln_b))
+    res, y, bias, ln_w, ln_b = _aligned16(res, y, bias, ln_w, ln_b)
     _contig(res, y, bias, ln_w, ln_b)
     dt = _dtype(res, y, bias, ln_w, ln_b)
     c = res.shape[-1]
@@ -322,6 +333,7 @@ def relpos_softmax(scores: torch.Tensor, q: torch.Tensor, table: torch.Tensor, h
     scores: [BH, h*w, h*w] raw q.k^T; q: [BH, h*w, hd]; table: rel_pos_h rows then rel_pos_w rows,
     [(2h-1)+(2w-1), hd]. Returns [BH, h*w, h*w].
     """
+    scores, q, table = _aligned16(scores, q, table)
     _contig(scores, q, table)
     dt = _dtype(scores, q, table)
     bh, n, hd = q.shape
@@ -338,6 +350,7 @@ def qkv_split(y: torch.Tensor, bias: torch.Tensor, n: int, nh: int, hd: int):
     """y: [T, 3*nh*hd] (bias-free qkv projection of T = windows * n tokens) + bias[3*nh*hd] ->
     (q [BH, n, hd], kT [BH, hd, n], v [BH, n, hd]) with BH = windows * nh, views of one packed buffer."""
     y = y.contiguous()
+    y, bias = _aligned16(y, bias)
     _contig(y, bias)
     dt = _dtype(y, bias)
     t = y.shape[0]
@@ -355,6 +368,7 @@ def qkv_split_grid(y: torch.Tensor, bias: torch.Tensor, batch: int, gh: int, gw:
     (q [BH, ws*ws, hd], kT [BH, hd, ws*ws], v [BH, ws*ws, hd]) for the windows of the grid zero-padded to
     multiples of ws (padding tokens: the bias alone), BH = batch * ceil(gh/ws) * ceil(gw/ws) * nh."""
     y = y.contiguous()
+    y, bias = _aligned16(y, bias)
     _contig(y, bias)
     dt = _dtype(y, bias)
     if y.shape != (batch * gh * gw, 3 * nh * hd) or bias.shape != (3 * nh * hd,):
@@ -372,6 +386,7 @@ def window_merge(ctx: torch.Tensor, batch: int, gh: int, gw: int, ws: int, nh: i
     """ctx [BH, ws*ws, hd] in qkv_split_grid's window order -> [batch, gh, gw, nh*hd] (heads merged,
     windows back on the grid without their padding)."""
     ctx = ctx.contiguous()
+    ctx, = _aligned16(ctx)
     _contig(ctx)
     dt = _dtype(ctx)
     bh, n, hd = ctx.shape
@@ -405,6 +420,7 @@ def _flash(q, k, v, out, layout: str, scale: float, cos=None, sin=None, n_rope_q
             raise SamHipError("sam-rs HIP kernels need device tensors")
         if t.device != q.device:
             raise SamHipError(f"sam-rs HIP kernels need all operands on one device: {t.device} vs {q.device}")
+    q, k, v = _aligned16(q, k, v)
     dt = _dtype(q, k, v)
     if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
         raise SamHipError(f"flash-attn: incompatible q/k/v shapes {tuple(q.shape)}/{tuple(k.shape)}/{tuple(v.shape)}")
@@ -466,6 +482,7 @@ def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask=None) -> torch.
             raise SamHipError("sam-rs HIP kernels need device tensors")
         if t.device != q.device:
             raise SamHipError(f"sam-rs HIP kernels need all operands on one device: {t.device} vs {q.device}")
+    q, k, v = _aligned16(q, k, v)
     dt = _dtype(q, k, v)
     if mask.dtype != q.dtype:
         raise SamHipError(f"sdpa: the mask must have q's dtype {q.dtype}, got {mask.dtype}")
@@ -499,7 +516,7 @@ def _rope_tables(cos: torch.Tensor, sin: torch.Tensor, d: int, device):
         raise SamHipError("rope: the cos/sin tables are f32 (sam3/vision.rs:26-46)")
     if cos.device != device or sin.device != device:
         raise SamHipError("rope: the tables must be on the same device as x")
-    return cos.contiguous(), sin.contiguous()
+    return _aligned16(cos.contiguous(), sin.contiguous())
 
 
 def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_rot: int | None = None) -> torch.Tensor:
@@ -524,6 +541,7 @@ def qkv_rope(y: torch.Tensor, bias: torch.Tensor, cos: torch.Tensor, sin: torch.
     """kernels::qkv_rope (kernels.rs:1013-1037): y [T, 3*heads*hd] (bias-free fused qkv projection) + bias,
     2-D RoPE on q and k with f32 tables [n, hd] (token t uses row t % n) -> packed [3, T, heads, hd]."""
     y = y.contiguous()
+    y, bias = _aligned16(y, bias)
     _contig(y, bias)
     dt = _dtype(y, bias)
     t = y.shape[0]

@@ -1,10 +1,10 @@
 """Parity of bias_residual and bias_gelu (libsam_hip.so) with the CPU oracle, on an MI355X.
 
 bias_residual is (res + y) + bias in f32 rounded once: bit-identical to the oracle in f32 and to the
-oracle's value rounded to nearest even in f16 / bf16. bias_gelu calls the device erff where the
-reference calls the `libm` crate's and the oracle the C library's; all are faithful to about an ulp,
-and the formula amplifies that for negative inputs, so gelu is held to a relative bar with an absolute
-floor (below). Cases: the ViT-H shapes (tokens x
+oracle's value rounded to nearest even in f16 / bf16. bias_gelu evaluates erf through a Chebyshev fit
+of erfc (fractional error below 1.2e-7) where the reference calls the `libm` crate's erf and the
+oracle the C library's; the formula amplifies such differences for negative inputs, so gelu is held to
+a relative bar with an absolute floor (below). Cases: the ViT-H shapes (tokens x
 1280 after attention, tokens x 5120 in the MLP), odd channel counts that take the scalar loop,
 misaligned views, in-place use and the argument errors.
 

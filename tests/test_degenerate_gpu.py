@@ -230,3 +230,39 @@ def test_bias_residual_ln_constant_rows(hip, c, dtype):
     torch.cuda.synchronize()
     assert (x == 0.5).all()
     assert torch.equal(normed, ln_b.expand(rows, c))
+
+
+def offset_view(x):
+    """x copied into a buffer one element past a 16-byte boundary: a contiguous view with a storage
+    offset, as candle's narrow of a packed tensor produces."""
+    buf = torch.empty(x.numel() + 1, dtype=x.dtype, device=x.device)
+    v = buf[1:].view(x.shape)
+    v.copy_(x)
+    assert v.data_ptr() % 16 != 0
+    return v
+
+
+def test_views_off_a_16_byte_boundary(hip):
+    """The reference's kernels take views with a storage offset. The front end copies such an input to
+    an aligned buffer for the kernels that need 16-byte alignment (their C ABI entry points refuse it);
+    bias_residual and bias_gelu take it as it is, through a scalar loop that rounds as their vector loop
+    does. Either way the results equal those of aligned inputs bit for bit."""
+    g = torch.Generator(device="cuda").manual_seed(8100)
+    f16 = torch.float16
+    q, kt, v = (torch.randn(s, device="cuda", generator=g).to(f16) for s in ((50, 196, 80), (50, 80, 196), (50, 196, 80)))
+    t = (0.02 * torch.randn(54, 80, device="cuda", generator=g)).to(f16)
+    want = hip.attention_relpos(q, kt, v, t, 14, 14, 80 ** -0.5)
+    got = hip.attention_relpos(offset_view(q), offset_view(kt), offset_view(v), offset_view(t), 14, 14, 80 ** -0.5)
+    assert torch.equal(got, want)
+    fq, fk, fv = (torch.randn(s, device="cuda", generator=g).to(f16) for s in ((1, 300, 2, 64), (1, 900, 2, 64), (1, 900, 2, 64)))
+    assert torch.equal(hip.flash_attn(offset_view(fq), offset_view(fk), offset_view(fv)), hip.flash_attn(fq, fk, fv))
+    s = torch.randn(2, 196, 196, device="cuda", generator=g).to(f16)
+    sq = torch.randn(2, 196, 64, device="cuda", generator=g).to(f16)
+    st = torch.randn(54, 64, device="cuda", generator=g).to(f16)
+    assert torch.equal(hip.relpos_softmax(offset_view(s), offset_view(sq), offset_view(st), 14, 14, 0.125),
+                       hip.relpos_softmax(s, sq, st, 14, 14, 0.125))
+    y, b = torch.randn(196 * 4, 3 * 4 * 64, device="cuda", generator=g).to(f16), torch.randn(3 * 4 * 64, device="cuda", generator=g).to(f16)
+    for got_, want_ in zip(hip.qkv_split(offset_view(y), offset_view(b), 196, 4, 64), hip.qkv_split(y, b, 196, 4, 64)):
+        assert torch.equal(got_, want_)
+    assert torch.equal(hip.bias_gelu(offset_view(y), offset_view(b)), hip.bias_gelu(y, b))
+    assert torch.equal(hip.bias_residual(offset_view(y), offset_view(y), offset_view(b)), hip.bias_residual(y, y, b))
